@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X FP8 linear path on one GPU.
+
+A step is one pass of the decode workload: the six 9B-class projections
+(q, k, v: 4096->4096/1024/1024, o: 4096->4096, fused gate+up: 4096->24576,
+down: 12288->4096) each applied once to M = 16 tokens through the full path
+(per-token e4m3 quantization of the bf16 activations + FP8 x FP8 GEMM + scale
+epilogue -> bf16). Weights rotate over enough copies (>= 512 MB) that every
+step reads them from HBM, not the 256 MB Infinity Cache. Inputs are resident
+in HBM before timing starts.
+
+value      = algorithmic bytes of the six linears / step time (GB/s), with
+             bytes per linear = N*K (e4m3 W) + 4N (scales) + 2MK (bf16 x) + 2MN (bf16 y)
+roofline   = the dominant kernel (the fused gate+up decode GEMM), timed alone
+             with HIP events on its stream: algorithmic bytes / average launch
+             time vs 8 TB/s
+prefill    = the same six projections at M = 2048 (TFLOP/s, 2*M*N*K per
+             linear), with the gate+up prefill GEMM's roofline vs 5.0 PFLOP/s
+cpu_baseline = the CPU oracle's dequantize-then-matmul (numpy float32, BLAS
+             threads) on the same decode step, timed on the host for a bounded
+             number of steps
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "FP8 linear TFLOP/s (M=2048) and HBM GB/s (M<=16) on 1 MI355X; % of roofline"
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+ROTATE_BYTES = 512 << 20
+
+
+def linear_bytes(M: int, N: int, K: int) -> int:
+    return N * K + 4 * N + 2 * M * K + 2 * M * N
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_set(torch, synthetic, quantize_rows, M: int, case):
+    """Quantized weights (rotated copies) and bf16 activations for one workload."""
+    weights, xs = {}, {}
+    for name in synthetic.SHAPES:
+        x, w = case(name, M)
+        wq, sw = quantize_rows(w.cuda())
+        weights[name] = (wq, sw)
+        xs[name] = x.cuda()
+    per_copy = sum(wq.numel() for wq, _ in weights.values())
+    copies = max(2, -(-ROTATE_BYTES // per_copy) + 1)
+    rot = [weights] + [{n: (wq.clone(), sw.clone()) for n, (wq, sw) in weights.items()} for _ in range(copies - 1)]
+    return rot, xs, copies, per_copy
+
+
+def time_region(torch, fn, steps: int, warmup: int) -> float:
+    """ms per call of fn over `steps` calls, HIP events on the current stream."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def kernel_time(torch, fp8, rot, xq, sx, name: str, launches: int) -> float:
+    """Average duration (ms) of the GEMM kernel alone for projection `name`
+    (pre-quantized activations, so each call is one kernel launch)."""
+    def one(i):
+        wq, sw = rot[i % len(rot)][name]
+        fp8.fp8_matmul_quantized(xq, sx, wq, sw)
+    return time_region(torch, one, launches, warmup=10)
+
+
+def cpu_baseline(synthetic, M: int, budget_s: float) -> dict:
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    import oracle
+
+    cores = min(os.cpu_count() or 1, 16)
+    # one decode step's operands (same seeds as the GPU run), quantized by the oracle
+    ops = []
+    total_bytes = 0
+    for name, (N, K) in synthetic.SHAPES.items():
+        x, w = synthetic.decode_case(name, M)
+        wq, sw = oracle.quantize_rows(w.float().numpy())
+        ops.append((x.float().numpy(), wq, sw))
+        total_bytes += linear_bytes(M, N, K)
+    with threadpool_limits(limits=cores):
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            for xf, wq, sw in ops:
+                xq, sx = oracle.quantize_rows(xf)
+                y = oracle.dequant_matmul_f32(xq, sx, wq, sw)
+                oracle.f32_to_bf16(y)
+            steps += 1
+            elapsed = time.perf_counter() - t0
+            if elapsed >= budget_s or steps >= 50:
+                break
+    return {"value": round(total_bytes * steps / elapsed / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{steps} decode steps (M={M}, the six projections, per-call weight dequant + sgemm) in {elapsed:.1f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--rows", type=int, default=16, help="decode tokens per step")
+    ap.add_argument("--prefill-rows", type=int, default=2048)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the FP8 linear path on one GPU; runs on more than one GPU are not part of this build",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from jeeves_amd import fp8, synthetic
+    from jeeves_amd.fp8_weights import quantize_rows
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        return 2
+    dev_name = torch.cuda.get_device_name(0)
+    M = args.rows
+    log(f"bench: decode M={M} on {dev_name}")
+    rot, xs, copies, per_copy = build_set(torch, synthetic, quantize_rows, M, synthetic.decode_case)
+    step_bytes = sum(linear_bytes(M, *synthetic.SHAPES[n]) for n in synthetic.SHAPES)
+
+    def step(i):
+        ws = rot[i % copies]
+        for name in synthetic.SHAPES:
+            wq, sw = ws[name]
+            fp8.fp8_matmul(xs[name], wq, sw)
+
+    ms = time_region(torch, step, args.steps, args.warmup)
+    value = step_bytes / (ms * 1e-3) / 1e9
+    log(f"bench: decode step {ms * 1e3:.1f} us, {value:.0f} GB/s")
+
+    # dominant kernel alone: the gate+up decode GEMM
+    N, K = synthetic.SHAPES["gate_up"]
+    xq, sx = quantize_rows(xs["gate_up"])
+    k_ms = kernel_time(torch, fp8, rot, xq, sx, "gate_up", max(args.steps, 100))
+    k_bytes = linear_bytes(M, N, K)
+    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
+    log(f"bench: gate_up decode GEMM {k_ms * 1e3:.2f} us, {k_gbs:.0f} GB/s")
+    per_shape = {}
+    for name, (n_, k_) in synthetic.SHAPES.items():
+        q_, s_ = quantize_rows(xs[name])
+        t = kernel_time(torch, fp8, rot, q_, s_, name, 100)
+        per_shape[name] = {"us": round(t * 1e3, 2), "GB/s": round(linear_bytes(M, n_, k_) / (t * 1e-3) / 1e9, 1)}
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 (fp32 accumulate)",
+        "data": "synthetic (seeded random-init weights and activations)",
+        "config": {
+            "workload": f"decode M={M}: 9B-class FP8 linears q 4096->4096, k/v 4096->1024, o 4096->4096, gate+up "
+                        f"4096->24576, down 12288->4096, one pass each per step (quant + GEMM + epilogue), weights "
+                        f"rotated over {copies} copies ({copies * per_copy / 2**20:.0f} MiB)",
+            "tokens": M,
+            "device": dev_name,
+        },
+        "roofline": {"bound": "hbm", "kernel": "gemm_decode_kernel (gate+up, N=24576 K=4096)", "achieved": round(k_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_us": round(k_ms * 1e3, 3), "bytes_per_launch": k_bytes},
+        "decode_kernels": per_shape,
+    }
+
+    if not args.no_prefill:
+        Mp = args.prefill_rows
+        log(f"bench: prefill M={Mp}")
+        del rot
+        torch.cuda.empty_cache()
+        prot, pxs, pcopies, _ = build_set(torch, synthetic, quantize_rows, Mp, synthetic.prefill_case)
+        flops = sum(2 * Mp * n_ * k_ for n_, k_ in synthetic.SHAPES.values())
+
+        def pstep(i):
+            ws = prot[i % pcopies]
+            for name in synthetic.SHAPES:
+                wq, sw = ws[name]
+                fp8.fp8_matmul(pxs[name], wq, sw)
+
+        pms = time_region(torch, pstep, max(args.steps // 4, 20), 5)
+        pq, ps = quantize_rows(pxs["gate_up"])
+        pk = kernel_time(torch, fp8, prot, pq, ps, "gate_up", 50)
+        pk_tf = 2 * Mp * N * K / (pk * 1e-3) / 1e12
+        pshape = {}
+        for name, (n_, k_) in synthetic.SHAPES.items():
+            q_, s_ = quantize_rows(pxs[name])
+            t = kernel_time(torch, fp8, prot, q_, s_, name, 30)
+            pshape[name] = {"us": round(t * 1e3, 2), "TFLOP/s": round(2 * Mp * n_ * k_ / (t * 1e-3) / 1e12, 1)}
+        result["prefill"] = {
+            "tokens": Mp, "ms_per_step": round(pms, 4), "TFLOP/s": round(flops / (pms * 1e-3) / 1e12, 1),
+            "roofline": {"bound": "mfma", "kernel": "gemm_prefill_kernel (gate+up, N=24576 K=4096)", "achieved": round(pk_tf, 1),
+                         "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(pk_tf / FP8_PEAK_TFLOPS, 4),
+                         "avg_launch_us": round(pk * 1e3, 2)},
+            "kernels": pshape,
+        }
+        log(f"bench: prefill step {pms:.3f} ms, gate+up GEMM {pk_tf:.0f} TFLOP/s")
+
+    if not args.no_cpu_baseline:
+        log("bench: cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(synthetic, M, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

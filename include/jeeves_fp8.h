@@ -1,0 +1,126 @@
+/*
+ * jeeves_fp8.h -- C ABI of the MI355X (gfx950) FP8 linear-layer library
+ * (libjeeves_fp8.so).
+ *
+ * The reference's FP8 path (PostHog/jeeves, `--precision fp8`) is Python over
+ * Triton kernels; these entry points are what its Python layer would bind in
+ * their place (ctypes, see the wrapper in jeeves_amd/_lib.py). Each
+ * declaration names the reference interface it replaces.
+ *
+ * Conventions for every entry point:
+ *   - pointers are device pointers (HBM) unless stated; bf16 tensors are
+ *     passed as raw 16-bit storage, e4m3fn codes as bytes;
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream);
+ *   - calls only enqueue work on `stream`: no allocation, no host
+ *     synchronisation, so they may be captured into a HIP graph;
+ *   - the return value is a JV_* status; on failure jv_fp8_last_error()
+ *     returns a message for the calling thread;
+ *   - row strides (`ld*`) are in elements; rows of bf16 and e4m3 operands
+ *     must start on 16-byte boundaries (ld*elem_size % 16 == 0, base 16-byte
+ *     aligned).
+ */
+#ifndef JEEVES_FP8_H
+#define JEEVES_FP8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JV_OK 0
+#define JV_ERR_VALUE 1   /* invalid argument (the reference raises ValueError) */
+#define JV_ERR_RUNTIME 2 /* invalid state (the reference raises RuntimeError) */
+#define JV_ERR_HIP 3     /* a HIP launch or runtime call failed */
+
+/* K granularity of the GEMM (BLOCK_K, inference/fp8.py:26). */
+#define JV_FP8_BLOCK_K 128
+/* Rows at or below which the GEMM takes the HBM-bound decode kernel
+ * (the counterpart of SPLIT_K_MAX_ROWS's regime split, inference/fp8.py:20). */
+#define JV_FP8_DECODE_MAX_ROWS 64
+/* Tile counters a stream needs at most (TILE_COUNTER_SLOTS, inference/fp8.py:27). */
+#define JV_FP8_TILE_COUNTER_SLOTS 65536
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* jv_fp8_last_error(void);
+
+/* Compute units of HIP device `device` (-1 = current device).
+ * Replaces sm_count (model/triton_kernels.py:18-20). Returns <= 0 on error. */
+int jv_device_cu_count(int device);
+
+/* quantize_rows (inference/fp8_weights.py:16-19) on the device, for bf16 rows:
+ *   scales[r] = max(max_c |x[r,c]|, 1e-12) * fp32(1/448)
+ *   codes[r,c] = e4m3fn(x[r,c] / scales[r])   (IEEE quotient, RNE, NaN on overflow)
+ * x: [rows, cols] bf16, row stride ldx; codes: [rows, cols] bytes, row stride
+ * ldc; scales: [rows] fp32. cols must be a positive multiple of 8.
+ * Used for per-token activation quantization and for FP8Linear.load_weight
+ * (inference/fp8.py:164-166). */
+int jv_fp8_quantize_rows_bf16(const void* x, int64_t ldx, int64_t rows, int64_t cols, void* codes, int64_t ldc,
+                              float* scales, void* stream);
+
+/* Same for float32 rows (FP8Linear.load_weight given fp32 weights). cols must be a
+ * positive multiple of 4. */
+int jv_fp8_quantize_rows_f32(const float* x, int64_t ldx, int64_t rows, int64_t cols, void* codes, int64_t ldc,
+                             float* scales, void* stream);
+
+/* Workspace bytes jv_fp8_linear needs for these sizes (activation codes and
+ * scales, LoRA low-rank activations, split-K partials). */
+int64_t jv_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t lora_rank);
+
+/* fp8_matmul (inference/fp8.py:112-148) plus FP8Linear.forward's bias
+ * (inference/fp8.py:183-184) and an optional LoRA adapter
+ * (model/lora.py:122-133), as one call:
+ *   per-token quantization of x (quantize_rows semantics), then
+ *   y[m,n] = bf16( acc[m,n] * sx[m] * w_scale[n] + bias[n]
+ *                  + lora_scaling * sum_r (x A^T)[m,r] * B[n,r] ),
+ *   acc[m,n] = sum_k xq[m,k] * w[n,k]  (e4m3 x e4m3, fp32 accumulation).
+ * x: [M,K] bf16 (row stride ldx); w: [N,K] e4m3fn (row stride ldw);
+ * w_scale: [N] fp32; bias: [N] bf16 or NULL; lora_a: [rank,K] bf16 and
+ * lora_b: [N,rank] bf16, or NULL with lora_rank 0 (rank 16 supported);
+ * y: [M,N] bf16 (row stride ldy).
+ * K must be a positive multiple of 128 (JV_ERR_VALUE otherwise, the
+ * ValueError of inference/fp8.py:115-117). workspace must hold
+ * jv_fp8_linear_workspace_bytes(M,N,K,rank) bytes (256-byte aligned).
+ * tile_counters: n_counters int32 slots, zero before first use, owned by one
+ * stream (launches on different streams must not share them); kernels leave
+ * them zero. Results are deterministic for a given device CU count. */
+int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
+                  const void* lora_a, const void* lora_b, int64_t lora_rank, float lora_scaling, void* y, int64_t ldy,
+                  int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, int32_t* tile_counters,
+                  int64_t n_counters, void* stream);
+
+/* Workspace bytes jv_fp8_gemm needs (split-K partials only). */
+int64_t jv_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/* The GEMM and epilogue alone on already-quantized activations
+ * (_fp8_matmul, inference/fp8.py:62-99, with FP8 x FP8 operands):
+ * xq: [M,K] e4m3fn (row stride ldxq); x_scale: [M] fp32; lora_t: [M,rank]
+ * fp32 low-rank activations or NULL; other arguments as jv_fp8_linear. */
+int jv_fp8_gemm(const void* xq, int64_t ldxq, const float* x_scale, const void* w, int64_t ldw, const float* w_scale,
+                const void* bias, const float* lora_t, const void* lora_b, int64_t lora_rank, float lora_scaling, void* y,
+                int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                int32_t* tile_counters, int64_t n_counters, void* stream);
+
+/* SwiGLU between the gate/up and down projections (SwiGLU.forward,
+ * model/model.py:581-584) fused with the down projection's per-token
+ * quantization: h = bf16(bf16(silu(gate)) * up), then quantize_rows(h).
+ * gate, up: [M,I] bf16 (may be the two halves of one fused gate+up output);
+ * codes: [M,I]; scales: [M]; h_out: [M,I] bf16 copy of h or NULL; lora_a:
+ * [rank,I] bf16 with lora_t: [M,rank] fp32 output (h A^T), or NULL/0.
+ * I must be a positive multiple of 8 and at most 16384. */
+int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_t ldu, int64_t M, int64_t I, void* codes,
+                           int64_t ldc, float* scales, void* h_out, int64_t ldh, const void* lora_a, int64_t lora_rank,
+                           float* lora_t, void* stream);
+
+/* Dispatch introspection (the role of split_for, inference/fp8.py:105-109):
+ * the number of K splits across workgroups the GEMM uses for these sizes on a
+ * device with cu_count compute units (1 = no cross-workgroup split), and the
+ * tile counters it needs. */
+int jv_fp8_split_for(int64_t M, int64_t N, int64_t K, int cu_count);
+int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JEEVES_FP8_H */

@@ -1,0 +1,214 @@
+// C ABI of libjeeves_fp8.so (declared in include/jeeves_fp8.h): argument
+// validation, regime dispatch (decode vs prefill), workspace carving, and
+// per-thread error messages. Launches only; no allocation, no host sync.
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/jeeves_fp8.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return JV_OK;
+  return fail(JV_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+
+int cu_count_of(int device) {
+  if (device < 0 && hipGetDevice(&device) != hipSuccess) return -1;
+  if (device >= kMaxDevices) return -1;
+  int v = g_cu_count[device].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0) return -1;
+  g_cu_count[device].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+int check_gemm_shape(int64_t M, int64_t N, int64_t K) {
+  if (K <= 0 || K % JV_FP8_BLOCK_K)
+    return fail(JV_ERR_VALUE, "the fp8 GEMM needs in_features divisible by %d, got %lld", JV_FP8_BLOCK_K, (long long)K);
+  if (M < 0 || N <= 0) return fail(JV_ERR_VALUE, "bad GEMM sizes M=%lld N=%lld", (long long)M, (long long)N);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return fail(JV_ERR_VALUE, "GEMM sizes exceed int32");
+  return JV_OK;
+}
+
+// Bytes of the split-K partials for these sizes (0 when no split).
+int64_t partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
+  if (M > jv::kDecodeMaxRows) return 0;
+  const int s = jv::decode_splits(N, K, cus);
+  return s > 1 ? round_up((int64_t)s * M * N * 4, 256) : 0;
+}
+
+int run_gemm(const uint8_t* xq, int64_t ldxq, const float* sx, const uint8_t* w, int64_t ldw, const float* sw,
+             const uint16_t* bias, const float* lora_t, const uint16_t* lora_b, int64_t rank, float lora_scaling, uint16_t* y,
+             int64_t ldy, int64_t M, int64_t N, int64_t K, uint8_t* partial_ws, int64_t partial_ws_bytes,
+             int32_t* counters, int64_t n_counters, hipStream_t stream) {
+  const int cus = cu_count_of(-1);
+  if (cus <= 0) return fail(JV_ERR_HIP, "cannot query the device's compute units");
+  if ((uint64_t)N * (uint64_t)ldw >= (1ull << 32) || (uint64_t)M * (uint64_t)ldxq >= (1ull << 32))
+    return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
+  jv::Epilogue ep{sx, sw, bias, lora_t, lora_b, lora_scaling, y, ldy};
+  if (M <= jv::kDecodeMaxRows) {
+    const int splits = jv::decode_splits(N, K, cus);
+    float* partial = nullptr;
+    if (splits > 1) {
+      const int64_t tiles = (N + 15) / 16;
+      if (!counters || tiles > n_counters)
+        return fail(JV_ERR_VALUE, "%lld tiles exceed the %lld tile counters", (long long)tiles, (long long)n_counters);
+      const int64_t need = (int64_t)splits * M * N * 4;
+      if (!partial_ws || partial_ws_bytes < need)
+        return fail(JV_ERR_VALUE, "workspace too small for split-K partials: %lld < %lld bytes", (long long)partial_ws_bytes,
+                    (long long)need);
+      partial = reinterpret_cast<float*>(partial_ws);
+    }
+    return hip_status(jv::gemm_decode(xq, ldxq, w, ldw, (int)M, (int)N, (int)K, splits, partial, counters, ep, (int)rank, stream),
+                      "fp8 decode GEMM launch");
+  }
+  const jv::PrefillTile tile = jv::prefill_tile(M, N, cus);
+  return hip_status(jv::gemm_prefill(xq, ldxq, w, ldw, (int)M, (int)N, (int)K, ep, (int)rank, tile, stream),
+                    "fp8 prefill GEMM launch");
+}
+
+int check_lora(int64_t rank, const void* a_or_t, const void* b) {
+  if (rank == 0) return JV_OK;
+  if (rank != 16) return fail(JV_ERR_VALUE, "LoRA rank %lld is not supported (16 is)", (long long)rank);
+  if (!a_or_t || !b) return fail(JV_ERR_VALUE, "LoRA rank %lld given without its matrices", (long long)rank);
+  return JV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* jv_fp8_last_error(void) { return g_last_error; }
+
+int jv_device_cu_count(int device) { return cu_count_of(device); }
+
+int jv_fp8_quantize_rows_bf16(const void* x, int64_t ldx, int64_t rows, int64_t cols, void* codes, int64_t ldc,
+                              float* scales, void* stream) {
+  if (rows < 0 || cols <= 0 || cols % 8 || cols > INT32_MAX || rows > INT32_MAX)
+    return fail(JV_ERR_VALUE, "quantize_rows needs a positive column count divisible by 8, got %lld", (long long)cols);
+  if (rows == 0) return JV_OK;
+  if (!aligned16(x) || (ldx * 2) % 16 || !aligned16(codes) || ldc % 16)
+    return fail(JV_ERR_VALUE, "quantize_rows needs 16-byte aligned rows");
+  return hip_status(jv::quant_rows_bf16((const uint16_t*)x, ldx, rows, (int)cols, (uint8_t*)codes, ldc, scales, nullptr, 0,
+                                        nullptr, (hipStream_t)stream),
+                    "quantize_rows launch");
+}
+
+int jv_fp8_quantize_rows_f32(const float* x, int64_t ldx, int64_t rows, int64_t cols, void* codes, int64_t ldc,
+                             float* scales, void* stream) {
+  if (rows < 0 || cols <= 0 || cols % 4 || cols > INT32_MAX || rows > INT32_MAX)
+    return fail(JV_ERR_VALUE, "quantize_rows needs a positive column count divisible by 4, got %lld", (long long)cols);
+  if (rows == 0) return JV_OK;
+  if (!aligned16(x) || (ldx * 4) % 16 || (reinterpret_cast<uintptr_t>(codes) & 3) || ldc % 4)
+    return fail(JV_ERR_VALUE, "quantize_rows needs 16-byte aligned rows");
+  return hip_status(jv::quant_rows_f32(x, ldx, rows, (int)cols, (uint8_t*)codes, ldc, scales, (hipStream_t)stream),
+                    "quantize_rows launch");
+}
+
+int64_t jv_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  const int cus = cu_count_of(-1);
+  if (cus <= 0) return -1;
+  return partial_bytes(M, N, K, cus);
+}
+
+int64_t jv_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t lora_rank) {
+  const int cus = cu_count_of(-1);
+  if (cus <= 0) return -1;
+  return round_up(M * K, 256) + round_up(M * 4, 256) + round_up(M * lora_rank * 4, 256) + partial_bytes(M, N, K, cus);
+}
+
+int jv_fp8_gemm(const void* xq, int64_t ldxq, const float* x_scale, const void* w, int64_t ldw, const float* w_scale,
+                const void* bias, const float* lora_t, const void* lora_b, int64_t lora_rank, float lora_scaling, void* y,
+                int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                int32_t* tile_counters, int64_t n_counters, void* stream) {
+  if (int rc = check_gemm_shape(M, N, K)) return rc;
+  if (int rc = check_lora(lora_rank, lora_t, lora_b)) return rc;
+  if (M == 0) return JV_OK;
+  if (!aligned16(xq) || ldxq % 16 || !aligned16(w) || ldw % 16)
+    return fail(JV_ERR_VALUE, "the fp8 GEMM needs 16-byte aligned operand rows");
+  return run_gemm((const uint8_t*)xq, ldxq, x_scale, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t,
+                  (const uint16_t*)lora_b, lora_rank, lora_scaling, (uint16_t*)y, ldy, M, N, K, (uint8_t*)workspace,
+                  workspace_bytes, tile_counters, n_counters, (hipStream_t)stream);
+}
+
+int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
+                  const void* lora_a, const void* lora_b, int64_t lora_rank, float lora_scaling, void* y, int64_t ldy,
+                  int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, int32_t* tile_counters,
+                  int64_t n_counters, void* stream) {
+  if (int rc = check_gemm_shape(M, N, K)) return rc;
+  if (int rc = check_lora(lora_rank, lora_a, lora_b)) return rc;
+  if (M == 0) return JV_OK;
+  if (!aligned16(x) || (ldx * 2) % 16 || !aligned16(w) || ldw % 16)
+    return fail(JV_ERR_VALUE, "the fp8 GEMM needs 16-byte aligned operand rows");
+  if (lora_rank && jv::quant_chunks((int)K) == 0)
+    return fail(JV_ERR_VALUE, "LoRA needs in_features <= 16384, got %lld", (long long)K);
+  const int64_t need = jv_fp8_linear_workspace_bytes(M, N, K, lora_rank);
+  if (need < 0) return fail(JV_ERR_HIP, "cannot query the device's compute units");
+  if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255))
+    return fail(JV_ERR_VALUE, "workspace needs %lld bytes, 256-byte aligned", (long long)need);
+  uint8_t* ws = (uint8_t*)workspace;
+  uint8_t* codes = ws;
+  ws += round_up(M * K, 256);
+  float* sx = (float*)ws;
+  ws += round_up(M * 4, 256);
+  float* lora_t = lora_rank ? (float*)ws : nullptr;
+  ws += round_up(M * lora_rank * 4, 256);
+  const int64_t rest = workspace_bytes - (ws - (uint8_t*)workspace);
+  hipStream_t s = (hipStream_t)stream;
+  if (int rc = hip_status(jv::quant_rows_bf16((const uint16_t*)x, ldx, M, (int)K, codes, K, sx, (const uint16_t*)lora_a,
+                                              (int)lora_rank, lora_t, s),
+                          "activation quantization launch"))
+    return rc;
+  return run_gemm(codes, K, sx, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t, (const uint16_t*)lora_b,
+                  lora_rank, lora_scaling, (uint16_t*)y, ldy, M, N, K, ws, rest, tile_counters, n_counters, s);
+}
+
+int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_t ldu, int64_t M, int64_t I, void* codes,
+                           int64_t ldc, float* scales, void* h_out, int64_t ldh, const void* lora_a, int64_t lora_rank,
+                           float* lora_t, void* stream) {
+  if (M < 0 || I <= 0 || I % 8 || jv::quant_chunks((int)(I > INT32_MAX ? 0 : I)) == 0 || I > INT32_MAX)
+    return fail(JV_ERR_VALUE, "swiglu_quantize needs 0 < I <= 16384 divisible by 8, got %lld", (long long)I);
+  if (int rc = check_lora(lora_rank, lora_a, lora_t)) return rc;
+  if (M == 0) return JV_OK;
+  if (!aligned16(gate) || (ldg * 2) % 16 || !aligned16(up) || (ldu * 2) % 16 || !aligned16(codes) || ldc % 16 ||
+      (h_out && (!aligned16(h_out) || (ldh * 2) % 16)))
+    return fail(JV_ERR_VALUE, "swiglu_quantize needs 16-byte aligned rows");
+  return hip_status(jv::quant_swiglu_bf16((const uint16_t*)gate, ldg, (const uint16_t*)up, ldu, M, (int)I, (uint8_t*)codes,
+                                          ldc, scales, (uint16_t*)h_out, ldh, (const uint16_t*)lora_a, (int)lora_rank,
+                                          lora_t, (hipStream_t)stream),
+                    "swiglu_quantize launch");
+}
+
+int jv_fp8_split_for(int64_t M, int64_t N, int64_t K, int cu_count) {
+  if (M > jv::kDecodeMaxRows || K <= 0 || N <= 0) return 1;
+  return jv::decode_splits(N, K, cu_count);
+}
+
+int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count) {
+  return jv_fp8_split_for(M, N, K, cu_count) > 1 ? (N + 15) / 16 : 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,139 @@
+// Shared device helpers for the gfx950 FP8 linear-layer kernels.
+//
+// Data conventions on the device:
+//   bf16     uint16_t bit patterns
+//   e4m3fn   uint8_t codes (OCP FP8 E4M3, "fn": no infinities, NaN = S.1111.111)
+//   scales   float32
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jv {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// fp32(1/448): the reciprocal that inference/fp8_weights.py:10 multiplies by.
+// The division is constant-folded with IEEE rounding, giving 0x3B124925.
+constexpr float kFp8MaxReciprocal = 1.0f / 448.0f;
+// fp32(1e-12): the clamp of inference/fp8_weights.py:18.
+constexpr float kScaleClampMin = 1e-12f;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// float -> bf16, round to nearest even; NaN -> 0x7FC0 (torch's c10::BFloat16).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t b = __float_as_uint(f);
+  if (f != f) return 0x7FC0u;
+  return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+// ---------------------------------------------------------------------------
+// e4m3fn encode, round to nearest even, NaN on overflow (|f| > 464), sign kept.
+// Written from the OCP FP8 v1.0 format definition; this is the semantics of
+// torch's float -> float8_e4m3fn cast that the reference quantizer uses.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t e4m3_encode_sw(float f) {
+  const uint32_t b = __float_as_uint(f);
+  const uint32_t sign = (b >> 24) & 0x80u;
+  const uint32_t mb = b & 0x7FFFFFFFu;
+  const float mag = __uint_as_float(mb);
+  uint32_t code;
+  if (!(mag <= 464.0f)) {
+    code = 0x7Fu;
+  } else if (mag < 0.015625f) {
+    // Subnormal codes m * 2^-9: m = rne(|f| * 2^9) in 0..8 (8 is the smallest normal).
+    code = (uint32_t)__builtin_rintf(mag * 512.0f);
+  } else {
+    // Round the 23-bit mantissa to 3 bits on the exponent|mantissa field (a carry
+    // bumps the exponent), then rebias 127 -> 7.
+    code = ((mb + 0x7FFFFu + ((mb >> 20) & 1u)) >> 20) - ((127u - 7u) << 3);
+  }
+  return code | sign;
+}
+
+// gfx950's v_cvt_pk_fp8_f32 (OCP e4m3, round to nearest even). Two floats into
+// two bytes of a 32-bit word; `hi` selects the upper 16 bits. The quantizer
+// only sends it finite quotients with |q| <= 448 * (1 + 2^-22), where its
+// result equals e4m3_encode_sw on every input (checked exhaustively over
+// that range by the conformance tests).
+template <bool HI>
+__device__ __forceinline__ int cvt_pk_fp8(float a, float b, int old) {
+  return __builtin_amdgcn_cvt_pk_fp8_f32(a, b, old, HI);
+}
+
+// ---------------------------------------------------------------------------
+// The quantizer's division x / scale for finite nonzero `scale` with
+// r = RN(1/scale): one product and two FMAs (Markstein's correction), with the
+// sign of x put back (callers apply copysign). For every pair of a bf16 x and
+// a bf16 row maximum it equals the IEEE quotient bit for bit wherever either
+// has magnitude >= 2^-11, and its e4m3 code equals the IEEE quotient's code
+// for every pair (both checked exhaustively by the tests). Rows whose scale is
+// inf or NaN take the plain IEEE division instead.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float quotient(float x, float scale, float r) {
+  const float q0 = x * r;
+  const float e = __builtin_fmaf(-q0, scale, x);
+  return __builtin_fmaf(e, r, q0);
+}
+
+// The reference's per-row scale from the row's largest magnitude, given as the
+// 15-bit bf16 magnitude pattern. NaN propagates as torch's amax and clamp do.
+__device__ __forceinline__ float scale_from_amax_bits(uint32_t amax_bits) {
+  const float amax = __uint_as_float(amax_bits << 16);
+  if (amax_bits > 0x7F80u) return amax;  // NaN
+  return fmaxf(amax, kScaleClampMin) * kFp8MaxReciprocal;
+}
+
+// Same for a float32 row maximum (already |.|), NaN-propagating.
+__device__ __forceinline__ float scale_from_amax_f32(float amax) {
+  if (amax != amax) return amax;
+  return fmaxf(amax, kScaleClampMin) * kFp8MaxReciprocal;
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Max of two packed 16-bit magnitudes (v_pk_max_u16).
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  u16x2 va = __builtin_bit_cast(u16x2, a);
+  u16x2 vb = __builtin_bit_cast(u16x2, b);
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(va, vb));
+}
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers. Format code 0 selects FP8 E4M3 for both operands; zero scale
+// operands select the unscaled v_mfma_f32_{32x32x64,16x16x128}_f8f6f4.
+// Each lane supplies 32 consecutive-k bytes of one row of A and of one column
+// of B; A and B use the same lane -> k mapping, so the k order inside the
+// instruction never changes the product.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x16 mfma_32x32x64_fp8(i32x8 a, i32x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma_16x16x128_fp8(i32x8 a, i32x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+__device__ __forceinline__ i32x8 cat8(i32x4 lo, i32x4 hi) {
+  return i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+}
+
+}  // namespace jv

@@ -1,0 +1,314 @@
+"""Drop-in for ``inference/fp8.py``: the FP8 linear layer on MI355X.
+
+Same public names and behaviour as the reference module -- ``fp8_matmul``,
+``FP8Linear`` (``load_codes``, ``load_weight``, ``concatenated``,
+``forward``), ``load_view``, ``warm``, ``split_for``, ``TILE_COUNTERS`` and
+the module constants -- with the Triton kernels replaced by the gfx950 HIP
+kernels of ``libjeeves_fp8.so``, called through its C ABI:
+
+* activations are quantized per token to e4m3fn with ``quantize_rows``
+  semantics (``inference/fp8_weights.py:16-19``) instead of being converted
+  to fp16 with a power-of-two row scale (``inference/fp8.py:46-58``);
+* the GEMM multiplies e4m3 by e4m3 on the FP8 MFMA units and applies
+  ``acc * sx[m] * sw[n]`` (+ bias, + optional LoRA) in its epilogue;
+* M <= ``DECODE_MAX_ROWS`` runs the HBM-bound split-K decode kernel, larger M
+  the LDS-tiled prefill kernel.
+
+Everything is enqueued on ``torch.cuda.current_stream()`` without host
+synchronisation; outputs and workspaces come from torch's caching allocator
+(or the graph pool under capture).
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .device import sm_count
+from .fp8_weights import FP8, quantize_rows
+
+# Rows at or below which fp8_matmul takes the decode kernel (the role of
+# SPLIT_K_MAX_ROWS, inference/fp8.py:20): up to four 16-token MFMA column tiles.
+DECODE_MAX_ROWS = 64
+BLOCK_K = 128
+TILE_COUNTER_SLOTS = 1 << 16
+# One row count per kernel variant: 1-4 decode token tiles, then prefill
+# batches that select the 256x256, 256x128 and 128x128 tiles on large and
+# small N (inference/fp8.py:32 plays the same role for Triton's JIT).
+WARM_ROWS = (1, 16, 17, 32, 33, 48, 49, 64, 65, 256, 300, 2048)
+LORA_RANKS = (16,)
+
+TILE_COUNTERS: dict[tuple[torch.device, int], torch.Tensor] = {}
+
+
+def split_for(N: int, K: int, sms: int) -> int:
+    """K splits across workgroups of the decode kernel for an (N, K) weight on a
+    device with ``sms`` compute units (``inference/fp8.py:105-109``'s role)."""
+    return _lib.lib().jv_fp8_split_for(1, N, K, sms)
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _tile_counters(device: torch.device, M: int, N: int, K: int) -> torch.Tensor | None:
+    need = _lib.lib().jv_fp8_counters_needed(M, N, K, sm_count(device))
+    if need <= 0:
+        return None
+    # Launches on different streams can overlap and must not share tile
+    # counters (inference/fp8.py:126), so they are kept per (device, stream).
+    key = (device, _stream(device))
+    counters = TILE_COUNTERS.get(key)
+    if counters is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("run an fp8 GEMM on this stream before capturing a CUDA graph on it, so that the stream's tile "
+                               "counters exist outside the graph")
+        counters = TILE_COUNTERS[key] = torch.zeros(TILE_COUNTER_SLOTS, dtype=torch.int32, device=device)
+    if need > counters.numel():
+        raise ValueError(f"{need} tiles exceed the {counters.numel()} tile counters")
+    return counters
+
+
+def _rows_aligned(t: torch.Tensor, elem: int) -> bool:
+    return t.stride(-1) == 1 and (t.stride(0) * elem) % 16 == 0 and t.data_ptr() % 16 == 0
+
+
+def _check_weight(K: int, weight: torch.Tensor) -> None:
+    if K == 0 or K % BLOCK_K or weight.dim() != 2 or weight.shape[1] != K:
+        raise ValueError(f"the fp8 GEMM needs in_features divisible by {BLOCK_K} and equal to the weight's, got {K} for a weight "
+                         f"of shape {tuple(weight.shape)}")
+
+
+def _check_lora(lora, K: int, N: int):
+    if lora is None:
+        return None, None, 0, 0.0
+    a, b, scaling = lora
+    r = a.shape[0]
+    if r not in LORA_RANKS or a.shape != (r, K) or b.shape != (N, r):
+        raise ValueError(f"LoRA factors must be A [r,{K}] and B [{N},r] with r in {LORA_RANKS}, got {tuple(a.shape)} and "
+                         f"{tuple(b.shape)}")
+    return a.to(torch.bfloat16).contiguous(), b.to(torch.bfloat16).contiguous(), r, float(scaling)
+
+
+def fp8_matmul(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *, bias: torch.Tensor | None = None,
+               lora: tuple[torch.Tensor, torch.Tensor, float] | None = None) -> torch.Tensor:
+    """``y = bf16(quant(x) @ weight^T * scale)`` (``inference/fp8.py:112-148``).
+
+    x: bf16 [M,K] with unit column stride (any 16-byte aligned row stride);
+    weight: float8_e4m3fn [N,K]; scale: float32 [N]. Returns a new bf16 [M,N]
+    on x's device; inputs are never written. ``bias`` (bf16 [N]) and ``lora``
+    (``(A [r,K], B [N,r], scaling)``) are folded into the same epilogue.
+    """
+    M, K = x.shape
+    N = weight.shape[0]
+    _check_weight(K, weight)
+    a, b, rank, scaling = _check_lora(lora, K, N)
+    dev = x.device
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    if not _rows_aligned(x, 2):
+        x = x.contiguous()
+    w = weight.view(torch.uint8)
+    if not _rows_aligned(w, 1):
+        w = w.contiguous()
+    y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    if M == 0:
+        return y
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+    scale = scale.to(torch.float32).contiguous()
+    L = _lib.lib()
+    with torch.cuda.device(dev):
+        counters = _tile_counters(dev, M, N, K)
+        ws_bytes = L.jv_fp8_linear_workspace_bytes(M, N, K, rank)
+        if ws_bytes < 0:
+            _lib.check(_lib.JV_ERR_HIP)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        _lib.check(L.jv_fp8_linear(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), scale.data_ptr(),
+                                   bias.data_ptr() if bias is not None else None, a.data_ptr() if rank else None,
+                                   b.data_ptr() if rank else None, rank, scaling, y.data_ptr(), N, M, N, K, ws.data_ptr(),
+                                   ws_bytes, _lib.counters_ptr(counters), counters.numel() if counters is not None else 0,
+                                   _stream(dev)))
+    return y
+
+
+def fp8_matmul_quantized(xq: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *,
+                         bias: torch.Tensor | None = None, lora_t: torch.Tensor | None = None,
+                         lora_b: torch.Tensor | None = None, lora_scaling: float = 0.0) -> torch.Tensor:
+    """The GEMM alone on activations already quantized per token (codes
+    float8_e4m3fn/uint8 [M,K] and scales float32 [M]), e.g. by
+    ``swiglu_quantize``. ``lora_t`` is ``x A^T`` (float32 [M,r])."""
+    M, K = xq.shape
+    N = weight.shape[0]
+    _check_weight(K, weight)
+    rank = 0 if lora_t is None else lora_t.shape[1]
+    if rank and (rank not in LORA_RANKS or lora_b is None or lora_b.shape != (N, rank)):
+        raise ValueError("lora_t needs lora_b [N, r] with r in (16,)")
+    dev = xq.device
+    xq = xq.view(torch.uint8)
+    if not _rows_aligned(xq, 1):
+        xq = xq.contiguous()
+    w = weight.view(torch.uint8)
+    if not _rows_aligned(w, 1):
+        w = w.contiguous()
+    y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    if M == 0:
+        return y
+    bias = bias.to(torch.bfloat16).contiguous() if bias is not None else None
+    if rank:
+        lora_t = lora_t.to(torch.float32).contiguous()
+        lora_b = lora_b.to(torch.bfloat16).contiguous()
+    L = _lib.lib()
+    with torch.cuda.device(dev):
+        counters = _tile_counters(dev, M, N, K)
+        ws_bytes = L.jv_fp8_gemm_workspace_bytes(M, N, K)
+        if ws_bytes < 0:
+            _lib.check(_lib.JV_ERR_HIP)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        _lib.check(L.jv_fp8_gemm(xq.data_ptr(), xq.stride(0), x_scale.to(torch.float32).contiguous().data_ptr(), w.data_ptr(),
+                                 w.stride(0), scale.to(torch.float32).contiguous().data_ptr(),
+                                 bias.data_ptr() if bias is not None else None, lora_t.data_ptr() if rank else None,
+                                 lora_b.data_ptr() if rank else None, rank, float(lora_scaling), y.data_ptr(), N, M, N, K,
+                                 ws.data_ptr(), ws_bytes, _lib.counters_ptr(counters),
+                                 counters.numel() if counters is not None else 0, _stream(dev)))
+    return y
+
+
+def swiglu_quantize(gate: torch.Tensor, up: torch.Tensor, *, lora_a: torch.Tensor | None = None,
+                    return_h: bool = False) -> tuple[torch.Tensor, ...]:
+    """``h = F.silu(gate) * up`` on bf16 (``model/model.py:583``) fused with the
+    down projection's per-token quantization. Returns ``(codes, scales)``, plus
+    ``t = h A^T`` (float32 [M,r]) when ``lora_a`` is given and ``h`` (bf16) when
+    ``return_h``."""
+    M, I = gate.shape
+    if up.shape != gate.shape:
+        raise ValueError(f"gate {tuple(gate.shape)} and up {tuple(up.shape)} differ")
+    dev = gate.device
+    gate, up = gate.to(torch.bfloat16), up.to(torch.bfloat16)
+    if not _rows_aligned(gate, 2):
+        gate = gate.contiguous()
+    if not _rows_aligned(up, 2):
+        up = up.contiguous()
+    codes = torch.empty(M, I, dtype=torch.uint8, device=dev)
+    scales = torch.empty(M, dtype=torch.float32, device=dev)
+    h = torch.empty(M, I, dtype=torch.bfloat16, device=dev) if return_h else None
+    rank = 0
+    t = None
+    if lora_a is not None:
+        rank = lora_a.shape[0]
+        if rank not in LORA_RANKS or lora_a.shape[1] != I:
+            raise ValueError(f"lora_a must be [r,{I}] with r in {LORA_RANKS}, got {tuple(lora_a.shape)}")
+        lora_a = lora_a.to(torch.bfloat16).contiguous()
+        t = torch.empty(M, rank, dtype=torch.float32, device=dev)
+    if M:
+        with torch.cuda.device(dev):
+            _lib.check(_lib.lib().jv_fp8_swiglu_quantize(gate.data_ptr(), gate.stride(0), up.data_ptr(), up.stride(0), M, I,
+                                                         codes.data_ptr(), I, scales.data_ptr(),
+                                                         h.data_ptr() if h is not None else None, I,
+                                                         lora_a.data_ptr() if rank else None, rank,
+                                                         t.data_ptr() if rank else None, _stream(dev)))
+    out: tuple[torch.Tensor, ...] = (codes.view(FP8), scales)
+    if rank:
+        out += (t,)
+    if return_h:
+        out += (h,)
+    return out
+
+
+class FP8Linear(nn.Module):
+    """``inference/fp8.py:151-185``: buffers ``weight`` (float8_e4m3fn [N,K])
+    and ``scale`` (float32 [N]), optional bf16 ``bias``. ``set_lora`` attaches
+    a LoRA adapter (``model/lora.py:122-133``) that the GEMM epilogue adds."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False, device: torch.device | str | None = None):
+        super().__init__()
+        self.register_buffer("weight", torch.empty(out_features, in_features, dtype=FP8, device=device))
+        self.register_buffer("scale", torch.empty(out_features, dtype=torch.float32, device=device))
+        self.bias = nn.Parameter(torch.empty(out_features, dtype=torch.bfloat16, device=device), requires_grad=False) if bias else None
+        self.in_features, self.out_features = in_features, out_features
+        self.lora: tuple[torch.Tensor, torch.Tensor, float] | None = None
+
+    @torch.no_grad()
+    def load_codes(self, codes: torch.Tensor, scale: torch.Tensor) -> None:
+        self.weight.copy_(codes)
+        self.scale.copy_(scale)
+
+    @torch.no_grad()
+    def load_weight(self, weight: torch.Tensor) -> None:
+        self.load_codes(*quantize_rows(weight.to(self.weight.device)))
+
+    def set_lora(self, a: torch.Tensor, b: torch.Tensor, scaling: float) -> None:
+        """Attach ``y += scaling * (x A^T) B^T`` (A [r,in], B [out,r], bf16)."""
+        _check_lora((a, b, scaling), self.in_features, self.out_features)
+        self.lora = (a.to(torch.bfloat16).contiguous(), b.to(torch.bfloat16).contiguous(), float(scaling))
+
+    @classmethod
+    def concatenated(cls, parts: list["FP8Linear"]) -> "FP8Linear":
+        sizes = [p.out_features for p in parts]
+        merged = cls(parts[0].in_features, sum(sizes), device="meta")
+        merged.weight, merged.scale = torch.cat([p.weight for p in parts]), torch.cat([p.scale for p in parts])
+        for p, weight, scale in zip(parts, merged.weight.split(sizes), merged.scale.split(sizes)):
+            p.weight, p.scale = weight, scale
+        return merged
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).to(torch.bfloat16)
+        if x2.stride(-1) != 1:
+            x2 = x2.contiguous()
+        y = fp8_matmul(x2, self.weight, self.scale, bias=self.bias, lora=self.lora)
+        return y.view(*shape[:-1], self.out_features)
+
+
+class FP8SwiGLU(nn.Module):
+    """``SwiGLU`` (``model/model.py:574-584``) over FP8 projections: one fused
+    gate+up GEMM (gate rows first, then up rows), the silu-product fused with
+    the down projection's activation quantization, then the down GEMM."""
+
+    def __init__(self, gate_up: FP8Linear, down: FP8Linear):
+        super().__init__()
+        if gate_up.out_features != 2 * down.in_features:
+            raise ValueError("gate_up must have twice down's in_features outputs")
+        self.gate_up, self.down = gate_up, down
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape
+        gu = self.gate_up(x.reshape(-1, shape[-1]))
+        inter = self.down.in_features
+        lora_a = self.down.lora[0] if self.down.lora is not None else None
+        out = swiglu_quantize(gu[:, :inter], gu[:, inter:], lora_a=lora_a)
+        lora_t = out[2] if lora_a is not None else None
+        y = fp8_matmul_quantized(out[0], out[1], self.down.weight, self.down.scale, bias=self.down.bias, lora_t=lora_t,
+                                 lora_b=self.down.lora[1] if lora_a is not None else None,
+                                 lora_scaling=self.down.lora[2] if lora_a is not None else 0.0)
+        return y.view(*shape[:-1], self.down.out_features)
+
+
+def load_view(model: str, drafter: str, block: int, device: torch.device):
+    """``inference/fp8.py:188-191``: the reference's FP8 loader with this
+    module's FP8Linear, then ``warm``. Needs the jeeves tree on ``sys.path``
+    (the loader, model and drafter are the caller's code)."""
+    try:
+        from inference.fp8_checkpoint import load_fp8_view
+    except ImportError as e:
+        raise ImportError("load_view builds the jeeves model with inference.fp8_checkpoint.load_fp8_view; run it from the "
+                          "jeeves tree") from e
+    view, head, encoder = load_fp8_view(model, drafter, block, device, FP8Linear)
+    warm(view)
+    return view, head, encoder
+
+
+@torch.no_grad()
+def warm(module: nn.Module) -> int:
+    """``inference/fp8.py:194-203``: run every distinct (N, K) at ``WARM_ROWS``
+    so each kernel variant has loaded and each stream's tile counters exist
+    before graph capture."""
+    seen = set()
+    for m in module.modules():
+        if isinstance(m, FP8Linear) and (m.out_features, m.in_features) not in seen:
+            seen.add((m.out_features, m.in_features))
+            w = m.weight
+            for rows in WARM_ROWS:
+                m(torch.zeros(rows, m.in_features, device=w.device, dtype=torch.bfloat16))
+    return len(seen)

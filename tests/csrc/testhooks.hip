@@ -1,0 +1,136 @@
+// Conformance probes for the GPU tests (built into tests/libjeeves_fp8_testhooks.so,
+// never shipped with the product library). They call the same device
+// functions as the product kernels (fp8_common.h):
+//   * th_encode: e4m3 encode of given floats by the hardware converter and by
+//     the spec encoder;
+//   * th_encode_sweep: every fp32 bit pattern in a range through both encoders,
+//     counting disagreements inside and outside the quantizer's domain;
+//   * th_quotient_sweep: every (bf16 x, bf16 row maximum) pair through the
+//     quantizer's fast quotient + hardware encode vs IEEE division + spec encode;
+//   * th_mfma32 / th_mfma16: one FP8 MFMA on lane-supplied operands, to check
+//     the output lane layout the GEMM epilogues assume.
+#include <stdint.h>
+
+#include "fp8_common.h"
+
+using namespace jv;
+
+namespace {
+
+__global__ void encode_kernel(const float* in, uint8_t* hw, uint8_t* sw, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float f = in[i];
+  hw[i] = (uint8_t)(cvt_pk_fp8<false>(f, 0.0f, 0) & 0xFF);
+  sw[i] = (uint8_t)e4m3_encode_sw(f);
+}
+
+__device__ __forceinline__ bool is_nan_code(uint32_t c) { return (c & 0x7F) == 0x7F; }
+
+// counts[0]: disagreements with |f| <= 449 (the quantizer's domain), counts[1]: elsewhere
+// (NaN codes compared by position only), counts[2]: number of domain inputs seen.
+__global__ void encode_sweep_kernel(uint32_t start, uint32_t n, unsigned long long* counts, uint32_t* first_bad) {
+  __shared__ unsigned long long s[3];
+  if (threadIdx.x < 3) s[threadIdx.x] = 0;
+  __syncthreads();
+  unsigned long long c0 = 0, c1 = 0, c2 = 0;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const uint32_t bits = start + i;
+    const float f = __uint_as_float(bits);
+    const uint32_t hw = (uint32_t)cvt_pk_fp8<false>(f, 0.0f, 0) & 0xFF;
+    const uint32_t sw = e4m3_encode_sw(f);
+    const bool same = hw == sw || (is_nan_code(hw) && is_nan_code(sw));
+    const bool domain = fabsf(f) <= 449.0f;
+    c2 += domain;
+    if (!same) {
+      if (domain) {
+        ++c0;
+        atomicMin(first_bad, bits);
+      } else {
+        ++c1;
+      }
+    }
+  }
+  atomicAdd(&s[0], c0);
+  atomicAdd(&s[1], c1);
+  atomicAdd(&s[2], c2);
+  __syncthreads();
+  if (threadIdx.x < 3) atomicAdd(&counts[threadIdx.x], s[threadIdx.x]);
+}
+
+// One block per row-maximum pattern a (bf16 magnitude 0 .. 0x7F7F); threads walk
+// every bf16 x with |x| <= a. counts[0]: quotient bit disagreements (finite-code
+// quotients only), counts[1]: code disagreements, counts[2]: pairs checked.
+__global__ void quotient_sweep_kernel(uint32_t a_begin, unsigned long long* counts, uint32_t* first_bad) {
+  __shared__ unsigned long long s[3];
+  if (threadIdx.x < 3) s[threadIdx.x] = 0;
+  __syncthreads();
+  const uint32_t amax_bits = a_begin + blockIdx.x;
+  const float scale = scale_from_amax_bits(amax_bits);
+  const float r = 1.0f / scale;
+  unsigned long long c0 = 0, c1 = 0, c2 = 0;
+  for (uint32_t xb = threadIdx.x; xb < 65536u; xb += blockDim.x) {
+    if ((xb & 0x7FFFu) > amax_bits) continue;
+    const float x = bf16_to_f32(xb);
+    const float exact = x / scale;
+    const float fast = __builtin_copysignf(quotient(x, scale, r), x);
+    const uint32_t code_exact = e4m3_encode_sw(exact);
+    const uint32_t code_fast = (uint32_t)cvt_pk_fp8<false>(fast, 0.0f, 0) & 0xFF;
+    ++c2;
+    if (__float_as_uint(exact) != __float_as_uint(fast)) ++c0;
+    if (code_exact != code_fast) {
+      ++c1;
+      atomicMin(first_bad, (amax_bits << 16) | xb);
+    }
+  }
+  atomicAdd(&s[0], c0);
+  atomicAdd(&s[1], c1);
+  atomicAdd(&s[2], c2);
+  __syncthreads();
+  if (threadIdx.x < 3) atomicAdd(&counts[threadIdx.x], s[threadIdx.x]);
+}
+
+__global__ void mfma32_kernel(const i32x8* a, const i32x8* b, f32x16* d) {
+  const int l = threadIdx.x;
+  f32x16 acc;
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  d[l] = mfma_32x32x64_fp8(a[l], b[l], acc);
+}
+
+__global__ void mfma16_kernel(const i32x8* a, const i32x8* b, f32x4* d) {
+  const int l = threadIdx.x;
+  d[l] = mfma_16x16x128_fp8(a[l], b[l], f32x4{0.f, 0.f, 0.f, 0.f});
+}
+
+}  // namespace
+
+extern "C" {
+
+int th_encode(const float* in, uint8_t* hw, uint8_t* sw, int64_t n, void* stream) {
+  if (n <= 0) return 0;
+  encode_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream>>>(in, hw, sw, n);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+int th_encode_sweep(uint32_t start, uint32_t n, unsigned long long* counts, uint32_t* first_bad, void* stream) {
+  encode_sweep_kernel<<<dim3(4096), dim3(256), 0, (hipStream_t)stream>>>(start, n, counts, first_bad);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+int th_quotient_sweep(uint32_t a_begin, uint32_t a_count, unsigned long long* counts, uint32_t* first_bad, void* stream) {
+  if (a_begin + a_count > 0x7F80u) return 1;
+  quotient_sweep_kernel<<<dim3(a_count), dim3(256), 0, (hipStream_t)stream>>>(a_begin, counts, first_bad);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+int th_mfma32(const void* a, const void* b, float* d, void* stream) {
+  mfma32_kernel<<<dim3(1), dim3(64), 0, (hipStream_t)stream>>>((const i32x8*)a, (const i32x8*)b, (f32x16*)d);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+int th_mfma16(const void* a, const void* b, float* d, void* stream) {
+  mfma16_kernel<<<dim3(1), dim3(64), 0, (hipStream_t)stream>>>((const i32x8*)a, (const i32x8*)b, (f32x4*)d);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+}  // extern "C"

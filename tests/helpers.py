@@ -1,0 +1,104 @@
+"""Shared helpers for the tests: torch <-> numpy views of bf16 / e4m3 data,
+the test-hook library, and the acceptance checks of the reference's tests."""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_int64, c_uint32, c_void_p
+from pathlib import Path
+
+import numpy as np
+import torch
+
+import oracle
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLDEN = ROOT / "tests" / "golden"
+HOOKS_PATH = ROOT / "tests" / "libjeeves_fp8_testhooks.so"
+
+_hooks = None
+
+
+def hooks() -> ctypes.CDLL:
+    global _hooks
+    if _hooks is None:
+        if not HOOKS_PATH.exists():
+            from jeeves_amd import build
+
+            build.build(tests=True)
+        h = ctypes.CDLL(str(HOOKS_PATH))
+        h.th_encode.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_void_p]
+        h.th_encode_sweep.argtypes = [c_uint32, c_uint32, c_void_p, c_void_p, c_void_p]
+        h.th_quotient_sweep.argtypes = [c_uint32, c_uint32, c_void_p, c_void_p, c_void_p]
+        h.th_mfma32.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p]
+        h.th_mfma16.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p]
+        for f in (h.th_encode, h.th_encode_sweep, h.th_quotient_sweep, h.th_mfma32, h.th_mfma16):
+            f.restype = c_int
+        _hooks = h
+    return _hooks
+
+
+def golden(name: str) -> dict[str, np.ndarray]:
+    with np.load(GOLDEN / name, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    """bf16 tensor -> uint16 bit patterns (host)."""
+    return t.detach().to(torch.bfloat16).cpu().contiguous().view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def codes_np(t: torch.Tensor) -> np.ndarray:
+    """e4m3fn / uint8 tensor -> uint8 codes (host)."""
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy().copy()
+
+
+def from_bits(b: np.ndarray, device="cpu") -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(b, dtype=np.uint16).view(np.int16)).view(torch.bfloat16).to(device)
+
+
+def same_codes(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Elementwise code equality, NaN codes compared by position only (the
+    reference's same_bits masks NaNs, model/triton_kernels_test.py:23-27)."""
+    nan_a = np.isnan(oracle.e4m3_decode(a))
+    nan_b = np.isnan(oracle.e4m3_decode(b))
+    return (a == b) | (nan_a & nan_b)
+
+
+def same_f32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    return (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def gemm_criteria(out_bits: np.ndarray, xq, sx, wq, sw, bias_bits=None, lora_term=None) -> dict:
+    """The acceptance numbers for one GEMM output:
+    * equal: share bitwise equal to the exact result rounded once to bf16
+      (inference/cuda_test.py:87-91);
+    * rel_l2: vs dequantize-then-matmul in float64;
+    * bound: |out - exact| <= |exact| 2^-8 + magnitude 2^-20 (model/metal_test.py:219-221)."""
+    exact = oracle.gemm_exact_f64(xq, sx, wq, sw)
+    if bias_bits is not None:
+        exact = exact + oracle.bf16_to_f32(bias_bits).astype(np.float64)[None, :]
+    if lora_term is not None:
+        exact = exact + lora_term
+    exact_bits = oracle.f64_to_bf16(exact)
+    out = oracle.bf16_to_f32(out_bits).astype(np.float64)
+    xd = np.abs(oracle.e4m3_decode(xq).astype(np.float64) * np.asarray(sx, np.float64)[:, None])
+    wd = np.abs(oracle.e4m3_decode(wq).astype(np.float64) * np.asarray(sw, np.float64)[:, None])
+    magnitude = xd @ wd.T
+    if bias_bits is not None:
+        magnitude = magnitude + np.abs(oracle.bf16_to_f32(bias_bits).astype(np.float64))[None, :]
+    if lora_term is not None:
+        magnitude = magnitude + np.abs(lora_term)
+    finite = np.isfinite(exact)
+    return {
+        "equal": oracle.bitwise_equal_fraction(out_bits, exact_bits),
+        "rel_l2": oracle.rel_l2(out[finite], exact[finite]) if finite.any() else 0.0,
+        "bound": oracle.within_metal_bound(out[finite], exact[finite], magnitude[finite]) if finite.any() else True,
+        "finite_match": bool((np.isfinite(out) == finite).all()),
+    }

@@ -1,0 +1,84 @@
+"""The C-ABI library loads on a host without a GPU, exports every symbol
+include/*.h declares, and validates arguments before touching the device."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from jeeves_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions() -> set[str]:
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(jv_\w+)\s*\(", text))
+    return names
+
+
+def test_header_declares_the_path():
+    names = declared_functions()
+    for required in ("jv_fp8_linear", "jv_fp8_gemm", "jv_fp8_quantize_rows_bf16", "jv_fp8_quantize_rows_f32",
+                     "jv_fp8_swiglu_quantize", "jv_device_cu_count", "jv_fp8_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(product_lib):
+    for name in declared_functions():
+        assert hasattr(product_lib, name), name
+
+
+def test_python_binding_matches_header():
+    assert set(_lib.SIGNATURES) == declared_functions()
+
+
+def test_library_is_gfx950_only():
+    data = _lib.LIB_PATH.read_bytes()
+    assert b"gfx950" in data
+    for other in (b"gfx942", b"gfx90a", b"sm_"):
+        assert other + b"\x00" not in data or other == b"sm_"
+
+
+def test_value_errors_need_no_device(product_lib):
+    L = product_lib
+    assert L.jv_fp8_quantize_rows_bf16(None, 0, 4, 7, None, 0, None, None) == _lib.JV_ERR_VALUE
+    assert b"divisible by 8" in L.jv_fp8_last_error()
+    rc = L.jv_fp8_linear(None, 0, None, 0, None, None, None, None, 0, 0.0, None, 0, 4, 64, 100, None, 0, None, 0, None)
+    assert rc == _lib.JV_ERR_VALUE
+    assert b"divisible by 128" in L.jv_fp8_last_error()
+    rc = L.jv_fp8_gemm(None, 0, None, None, 0, None, None, None, None, 8, 0.0, None, 0, 4, 64, 128, None, 0, None, 0, None)
+    assert rc == _lib.JV_ERR_VALUE and b"rank 8" in L.jv_fp8_last_error()
+    rc = L.jv_fp8_swiglu_quantize(None, 0, None, 0, 4, 20000, None, 0, None, None, 0, None, 0, None, None)
+    assert rc == _lib.JV_ERR_VALUE
+    # M = 0 is a no-op that succeeds
+    assert L.jv_fp8_linear(None, 0, None, 0, None, None, None, None, 0, 0.0, None, 0, 0, 64, 128, None, 0, None, 0, None) == 0
+
+
+def test_error_mapping():
+    with pytest.raises(ValueError):
+        _lib.lib().jv_fp8_quantize_rows_bf16(None, 0, 1, 3, None, 0, None, None) and _lib.check(_lib.JV_ERR_VALUE)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.JV_ERR_RUNTIME)
+    _lib.check(_lib.JV_OK)
+
+
+def test_split_for_is_pure_host_logic(product_lib):
+    L = product_lib
+    # 256 CUs: q/o (256 tiles of 16 rows) need no split; k/v (64 tiles) split 4 ways
+    assert L.jv_fp8_split_for(16, 4096, 4096, 256) == 1
+    assert L.jv_fp8_split_for(16, 1024, 4096, 256) == 4
+    assert L.jv_fp8_split_for(16, 24576, 4096, 256) == 1
+    assert L.jv_fp8_split_for(2048, 1024, 4096, 256) == 1  # prefill never splits
+    assert L.jv_fp8_counters_needed(16, 1024, 4096, 256) == 64
+    assert L.jv_fp8_counters_needed(16, 4096, 4096, 256) == 0
+
+
+def test_hook_library_exports(hooks_lib):
+    for name in ("th_encode", "th_encode_sweep", "th_quotient_sweep", "th_mfma32", "th_mfma16"):
+        assert hasattr(hooks_lib, name)

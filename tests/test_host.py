@@ -1,0 +1,109 @@
+"""Host-side logic of the drop-in module that runs without a GPU: the
+quantizability rule, module replacement, FP8Linear buffers and merges,
+argument validation, and the synthetic workload generators."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import jeeves_amd
+from jeeves_amd import synthetic
+from jeeves_amd.fp8 import FP8Linear, fp8_matmul
+from jeeves_amd.fp8_weights import FP8, FP8_MAX, FP8_MAX_RECIPROCAL, QUANTIZE_BLOCK_ROWS, SCALE_SUFFIX, quantizable, replace_linears
+
+
+def test_constants_match_reference():
+    assert FP8 is torch.float8_e4m3fn and FP8_MAX == 448.0
+    assert FP8_MAX_RECIPROCAL == float.fromhex("0x1.24924ap-9")
+    assert SCALE_SUFFIX == "_scale" and QUANTIZE_BLOCK_ROWS == 16384
+    assert jeeves_amd.BLOCK_K == 128 and jeeves_amd.TILE_COUNTER_SLOTS == 1 << 16
+
+
+def test_quantizable_and_replace_linears():
+    with torch.device("meta"):
+        model = nn.Sequential(nn.Linear(4096, 4096), nn.Sequential(nn.Linear(4096, 1024), nn.Linear(4096, 32)),
+                              nn.Linear(100, 2048), nn.Linear(4096, 1040))
+    assert quantizable(model[0]) and not quantizable(model[1][1]) and not quantizable(model[2])
+    n = replace_linears(model, lambda l: FP8Linear(l.in_features, l.out_features, bias=l.bias is not None, device="meta"))
+    assert n == 3
+    assert isinstance(model[0], FP8Linear) and isinstance(model[1][0], FP8Linear) and isinstance(model[3], FP8Linear)
+    assert isinstance(model[1][1], nn.Linear) and isinstance(model[2], nn.Linear)
+
+
+def test_fp8_linear_buffers_and_state_dict():
+    m = FP8Linear(256, 1024, bias=True, device="meta")
+    assert m.weight.dtype == FP8 and m.weight.shape == (1024, 256)
+    assert m.scale.dtype == torch.float32 and m.scale.shape == (1024,)
+    assert m.bias.dtype == torch.bfloat16 and not m.bias.requires_grad
+    assert set(m.state_dict()) == {"weight", "scale", "bias"}
+    assert set(FP8Linear(256, 1024).state_dict()) == {"weight", "scale"}
+
+
+def test_concatenated_parts_become_views():
+    # inference/cuda_test.py:38-46: merging keeps codes and scales and the parts view the merged storage
+    g = torch.Generator().manual_seed(0)
+    parts = []
+    for n in (64, 16, 16):
+        p = FP8Linear(128, n, device="cpu")
+        p.weight.copy_(torch.randint(0, 0x7E, (n, 128), generator=g, dtype=torch.uint8).view(FP8))
+        p.scale.copy_(torch.rand(n, generator=g))
+        parts.append(p)
+    codes = [p.weight.clone() for p in parts]
+    scales = [p.scale.clone() for p in parts]
+    merged = FP8Linear.concatenated(parts)
+    assert merged.out_features == 96 and merged.in_features == 128
+    for p, c, s in zip(parts, codes, scales):
+        assert torch.equal(p.weight.view(torch.uint8), c.view(torch.uint8)) and torch.equal(p.scale, s)
+        assert p.weight.untyped_storage().data_ptr() == merged.weight.untyped_storage().data_ptr()
+        assert p.scale.untyped_storage().data_ptr() == merged.scale.untyped_storage().data_ptr()
+
+
+def test_fp8_matmul_validates_before_launch():
+    x = torch.zeros(4, 100, dtype=torch.bfloat16)
+    w = torch.zeros(64, 100, dtype=torch.uint8).view(FP8)
+    with pytest.raises(ValueError, match="divisible by 128"):
+        fp8_matmul(x, w, torch.ones(64))
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="equal to the weight's"):
+        fp8_matmul(x, torch.zeros(64, 128, dtype=torch.uint8).view(FP8), torch.ones(64))
+    w = torch.zeros(64, 256, dtype=torch.uint8).view(FP8)
+    with pytest.raises(ValueError, match="LoRA"):
+        fp8_matmul(x, w, torch.ones(64), lora=(torch.zeros(8, 256), torch.zeros(64, 8), 2.0))
+
+
+def test_set_lora_validates_shapes():
+    m = FP8Linear(256, 1024, device="meta")
+    with pytest.raises(ValueError):
+        m.set_lora(torch.zeros(16, 128), torch.zeros(1024, 16), 2.0)
+    m.set_lora(torch.zeros(16, 256), torch.zeros(1024, 16), 2.0)
+    assert m.lora[2] == 2.0 and m.lora[0].dtype == torch.bfloat16
+
+
+def test_synthetic_generators_are_seeded():
+    x1, w1 = synthetic.single_linear()
+    x2, w2 = synthetic.single_linear()
+    assert torch.equal(x1, x2) and torch.equal(w1, w2)
+    assert x1.shape == (16, 4096) and w1.shape == (4096, 4096) and x1.dtype == torch.bfloat16
+    # 8 outlier channels scaled x20
+    col_std = x1.float().std(0)
+    assert (col_std > 5).sum() == 8
+    assert abs(w1.float().std().item() - 0.02) < 1e-3
+    xh = synthetic.activations_heavy_tail(512, 4096, 300 + 512).float()
+    kurt = ((xh - xh.mean(0)) ** 4).mean(0) / xh.var(0) ** 2
+    assert (kurt > 6).sum() >= 20  # the Student-t channels
+    lens = synthetic.ragged_lengths()
+    assert len(lens) == 64 and min(lens) >= 64 and max(lens) <= 2048
+    assert synthetic.SHAPES["gate_up"] == (24576, 4096) and synthetic.SHAPES["down"] == (4096, 12288)
+    a, b = synthetic.lora_factors(1024, 4096, 400)
+    assert a.shape == (16, 4096) and b.shape == (1024, 16)
+    assert abs(a.float().std().item() - 0.01) < 1e-3
+
+
+def test_decode_case_seeds_are_distinct():
+    xa, wa = synthetic.decode_case("q", 16)
+    xb, wb = synthetic.decode_case("o", 16)
+    assert torch.equal(xa, xb) and not torch.equal(wa, wb)
+    assert np.isfinite(xa.float().numpy()).all()
