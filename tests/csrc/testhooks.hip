@@ -97,6 +97,11 @@ __global__ void mfma32_kernel(const i32x8* a, const i32x8* b, f32x16* d) {
   d[l] = mfma_32x32x64_fp8(a[l], b[l], acc);
 }
 
+__global__ void mfma32_acc_kernel(const i32x8* a, const i32x8* b, const f32x16* c, f32x16* d) {
+  const int l = threadIdx.x;
+  d[l] = mfma_32x32x64_fp8(a[l], b[l], c[l]);
+}
+
 __global__ void mfma16_kernel(const i32x8* a, const i32x8* b, f32x4* d) {
   const int l = threadIdx.x;
   d[l] = mfma_16x16x128_fp8(a[l], b[l], f32x4{0.f, 0.f, 0.f, 0.f});
@@ -125,6 +130,12 @@ int th_quotient_sweep(uint32_t a_begin, uint32_t a_count, unsigned long long* co
 
 int th_mfma32(const void* a, const void* b, float* d, void* stream) {
   mfma32_kernel<<<dim3(1), dim3(64), 0, (hipStream_t)stream>>>((const i32x8*)a, (const i32x8*)b, (f32x16*)d);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+int th_mfma32_acc(const void* a, const void* b, const float* c, float* d, void* stream) {
+  mfma32_acc_kernel<<<dim3(1), dim3(64), 0, (hipStream_t)stream>>>((const i32x8*)a, (const i32x8*)b, (const f32x16*)c,
+                                                                   (f32x16*)d);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 
