@@ -5,18 +5,20 @@ A step is one pass of the decode workload: the six 9B-class projections
 (q, k, v: 4096->4096/1024/1024, o: 4096->4096, fused gate+up: 4096->24576,
 down: 12288->4096) each applied once to M = 16 tokens through the full path
 (per-token e4m3 quantization of the bf16 activations + FP8 x FP8 GEMM + scale
-epilogue -> bf16). Weights rotate over enough copies (>= 512 MB) that every
-step reads them from HBM, not the 256 MB Infinity Cache. Inputs are resident
-in HBM before timing starts.
+epilogue -> bf16). As in the reference engine, which replays its decode passes
+as CUDA graphs (inference/engine.py:351-360), each step is a captured HIP graph
+replay, so host launch overhead is not measured. Weights rotate over enough
+copies (>= 512 MB) that every step reads them from HBM, not the 256 MB
+Infinity Cache. Inputs are resident in HBM before timing starts.
 
-value      = algorithmic bytes of the six linears / step time (GB/s), with
+value        algorithmic bytes of the six linears / step time (GB/s), with
              bytes per linear = N*K (e4m3 W) + 4N (scales) + 2MK (bf16 x) + 2MN (bf16 y)
-roofline   = the dominant kernel (the fused gate+up decode GEMM), timed alone
-             with HIP events on its stream: algorithmic bytes / average launch
-             time vs 8 TB/s
-prefill    = the same six projections at M = 2048 (TFLOP/s, 2*M*N*K per
+roofline     the dominant kernel (the fused gate+up decode GEMM) alone: a graph
+             of back-to-back launches on rotated weights, timed with HIP events
+             on its stream; algorithmic bytes / average launch time vs 8 TB/s
+prefill      the same six projections at M = 2048 (TFLOP/s, 2*M*N*K per
              linear), with the gate+up prefill GEMM's roofline vs 5.0 PFLOP/s
-cpu_baseline = the CPU oracle's dequantize-then-matmul (numpy float32, BLAS
+cpu_baseline the CPU oracle's dequantize-then-matmul (numpy float32, BLAS
              threads) on the same decode step, timed on the host for a bounded
              number of steps
 
@@ -39,6 +41,7 @@ METRIC = "FP8 linear TFLOP/s (M=2048) and HBM GB/s (M<=16) on 1 MI355X; % of roo
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 ROTATE_BYTES = 512 << 20
+LAUNCHES_PER_GRAPH = 24
 
 
 def linear_bytes(M: int, N: int, K: int) -> int:
@@ -47,6 +50,41 @@ def linear_bytes(M: int, N: int, K: int) -> int:
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+class Bench:
+    def __init__(self, torch):
+        self.torch = torch
+        self.stream = torch.cuda.Stream()
+
+    def capture(self, fn):
+        """Capture fn() into a HIP graph on the bench stream (after one eager run
+        on that stream, which creates its tile counters outside the capture)."""
+        torch = self.torch
+        self.stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(self.stream):
+            fn()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=self.stream):
+                fn()
+        torch.cuda.current_stream().wait_stream(self.stream)
+        torch.cuda.synchronize()
+        return g
+
+    def time_graphs(self, graphs, replays: int, warmup: int) -> float:
+        """ms per replay, HIP events recorded on the stream the graphs replay on."""
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for i in range(warmup):
+                graphs[i % len(graphs)].replay()
+            self.stream.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(self.stream)
+            for i in range(replays):
+                graphs[i % len(graphs)].replay()
+            end.record(self.stream)
+            end.synchronize()
+        return start.elapsed_time(end) / replays
 
 
 def build_set(torch, synthetic, quantize_rows, M: int, case):
@@ -63,37 +101,25 @@ def build_set(torch, synthetic, quantize_rows, M: int, case):
     return rot, xs, copies, per_copy
 
 
-def time_region(torch, fn, steps: int, warmup: int) -> float:
-    """ms per call of fn over `steps` calls, HIP events on the current stream."""
-    for i in range(warmup):
-        fn(i)
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        fn(i)
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
-
-
-def kernel_time(torch, fp8, rot, xq, sx, name: str, launches: int) -> float:
-    """Average duration (ms) of the GEMM kernel alone for projection `name`
-    (pre-quantized activations, so each call is one kernel launch)."""
-    def one(i):
-        wq, sw = rot[i % len(rot)][name]
-        fp8.fp8_matmul_quantized(xq, sx, wq, sw)
-    return time_region(torch, one, launches, warmup=10)
+def kernel_ms(b: Bench, fp8, rot, xq, sx, name: str, replays: int) -> float:
+    """Average time (ms) of one GEMM kernel launch for projection `name` on
+    pre-quantized activations, from graphs of back-to-back launches."""
+    graphs = []
+    for c in range(len(rot)):
+        def launches(c=c):
+            for j in range(LAUNCHES_PER_GRAPH):
+                wq, sw = rot[(c + j) % len(rot)][name]
+                fp8.fp8_matmul_quantized(xq, sx, wq, sw)
+        graphs.append(b.capture(launches))
+    return b.time_graphs(graphs, replays, 3) / LAUNCHES_PER_GRAPH
 
 
 def cpu_baseline(synthetic, M: int, budget_s: float) -> dict:
-    import numpy as np
     from threadpoolctl import threadpool_limits
 
     import oracle
 
     cores = min(os.cpu_count() or 1, 16)
-    # one decode step's operands (same seeds as the GPU run), quantized by the oracle
     ops = []
     total_bytes = 0
     for name, (N, K) in synthetic.SHAPES.items():
@@ -106,24 +132,24 @@ def cpu_baseline(synthetic, M: int, budget_s: float) -> dict:
         while True:
             for xf, wq, sw in ops:
                 xq, sx = oracle.quantize_rows(xf)
-                y = oracle.dequant_matmul_f32(xq, sx, wq, sw)
-                oracle.f32_to_bf16(y)
+                oracle.f32_to_bf16(oracle.dequant_matmul_f32(xq, sx, wq, sw))
             steps += 1
             elapsed = time.perf_counter() - t0
             if elapsed >= budget_s or steps >= 50:
                 break
     return {"value": round(total_bytes * steps / elapsed / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"{steps} decode steps (M={M}, the six projections, per-call weight dequant + sgemm) in {elapsed:.1f} s"}
+            "sample": f"{steps} decode steps (M={M}, the six projections: per-token quant, per-call weight dequant, "
+                      f"float32 sgemm, bf16 rounding) in {elapsed:.1f} s"}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--rows", type=int, default=16, help="decode tokens per step")
     ap.add_argument("--prefill-rows", type=int, default=2048)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
@@ -140,34 +166,33 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP GPU", file=sys.stderr)
         return 2
+    b = Bench(torch)
     dev_name = torch.cuda.get_device_name(0)
     M = args.rows
     log(f"bench: decode M={M} on {dev_name}")
     rot, xs, copies, per_copy = build_set(torch, synthetic, quantize_rows, M, synthetic.decode_case)
     step_bytes = sum(linear_bytes(M, *synthetic.SHAPES[n]) for n in synthetic.SHAPES)
 
-    def step(i):
-        ws = rot[i % copies]
+    def step(c):
         for name in synthetic.SHAPES:
-            wq, sw = ws[name]
+            wq, sw = rot[c][name]
             fp8.fp8_matmul(xs[name], wq, sw)
 
-    ms = time_region(torch, step, args.steps, args.warmup)
+    graphs = [b.capture(lambda c=c: step(c)) for c in range(copies)]
+    ms = b.time_graphs(graphs, args.steps, args.warmup)
     value = step_bytes / (ms * 1e-3) / 1e9
     log(f"bench: decode step {ms * 1e3:.1f} us, {value:.0f} GB/s")
 
-    # dominant kernel alone: the gate+up decode GEMM
-    N, K = synthetic.SHAPES["gate_up"]
-    xq, sx = quantize_rows(xs["gate_up"])
-    k_ms = kernel_time(torch, fp8, rot, xq, sx, "gate_up", max(args.steps, 100))
-    k_bytes = linear_bytes(M, N, K)
-    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
-    log(f"bench: gate_up decode GEMM {k_ms * 1e3:.2f} us, {k_gbs:.0f} GB/s")
     per_shape = {}
     for name, (n_, k_) in synthetic.SHAPES.items():
         q_, s_ = quantize_rows(xs[name])
-        t = kernel_time(torch, fp8, rot, q_, s_, name, 100)
+        t = kernel_ms(b, fp8, rot, q_, s_, name, 40)
         per_shape[name] = {"us": round(t * 1e3, 2), "GB/s": round(linear_bytes(M, n_, k_) / (t * 1e-3) / 1e9, 1)}
+    N, K = synthetic.SHAPES["gate_up"]
+    k_ms = per_shape["gate_up"]["us"] * 1e-3
+    k_bytes = linear_bytes(M, N, K)
+    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
+    log(f"bench: decode GEMM kernels {per_shape}")
 
     result = {
         "metric": METRIC,
@@ -184,48 +209,48 @@ def main() -> int:
         "data": "synthetic (seeded random-init weights and activations)",
         "config": {
             "workload": f"decode M={M}: 9B-class FP8 linears q 4096->4096, k/v 4096->1024, o 4096->4096, gate+up "
-                        f"4096->24576, down 12288->4096, one pass each per step (quant + GEMM + epilogue), weights "
-                        f"rotated over {copies} copies ({copies * per_copy / 2**20:.0f} MiB)",
+                        f"4096->24576, down 12288->4096, one pass each per step (quant + GEMM + epilogue) replayed as "
+                        f"a HIP graph, weights rotated over {copies} copies ({copies * per_copy / 2**20:.0f} MiB)",
             "tokens": M,
             "device": dev_name,
         },
-        "roofline": {"bound": "hbm", "kernel": "gemm_decode_kernel (gate+up, N=24576 K=4096)", "achieved": round(k_gbs, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "avg_launch_us": round(k_ms * 1e3, 3), "bytes_per_launch": k_bytes},
+        "roofline": {"bound": "hbm", "kernel": "gemm_decode_kernel (gate+up, N=24576 K=4096, M=16)",
+                     "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "avg_launch_us": round(k_ms * 1e3, 3), "bytes_per_launch": k_bytes},
         "decode_kernels": per_shape,
     }
 
     if not args.no_prefill:
         Mp = args.prefill_rows
         log(f"bench: prefill M={Mp}")
-        del rot
+        del rot, graphs
         torch.cuda.empty_cache()
         prot, pxs, pcopies, _ = build_set(torch, synthetic, quantize_rows, Mp, synthetic.prefill_case)
         flops = sum(2 * Mp * n_ * k_ for n_, k_ in synthetic.SHAPES.values())
 
-        def pstep(i):
-            ws = prot[i % pcopies]
+        def pstep(c):
             for name in synthetic.SHAPES:
-                wq, sw = ws[name]
+                wq, sw = prot[c][name]
                 fp8.fp8_matmul(pxs[name], wq, sw)
 
-        pms = time_region(torch, pstep, max(args.steps // 4, 20), 5)
-        pq, ps = quantize_rows(pxs["gate_up"])
-        pk = kernel_time(torch, fp8, prot, pq, ps, "gate_up", 50)
-        pk_tf = 2 * Mp * N * K / (pk * 1e-3) / 1e12
+        pgraphs = [b.capture(lambda c=c: pstep(c)) for c in range(pcopies)]
+        pms = b.time_graphs(pgraphs, max(args.steps // 8, 20), 3)
         pshape = {}
         for name, (n_, k_) in synthetic.SHAPES.items():
             q_, s_ = quantize_rows(pxs[name])
-            t = kernel_time(torch, fp8, prot, q_, s_, name, 30)
+            t = kernel_ms(b, fp8, prot, q_, s_, name, 8)
             pshape[name] = {"us": round(t * 1e3, 2), "TFLOP/s": round(2 * Mp * n_ * k_ / (t * 1e-3) / 1e12, 1)}
+        pk = pshape["gate_up"]["us"] * 1e-3
+        pk_tf = 2 * Mp * N * K / (pk * 1e-3) / 1e12
         result["prefill"] = {
             "tokens": Mp, "ms_per_step": round(pms, 4), "TFLOP/s": round(flops / (pms * 1e-3) / 1e12, 1),
-            "roofline": {"bound": "mfma", "kernel": "gemm_prefill_kernel (gate+up, N=24576 K=4096)", "achieved": round(pk_tf, 1),
-                         "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(pk_tf / FP8_PEAK_TFLOPS, 4),
-                         "avg_launch_us": round(pk * 1e3, 2)},
+            "roofline": {"bound": "mfma", "kernel": "gemm_prefill_kernel (gate+up, N=24576 K=4096, M=2048)",
+                         "achieved": round(pk_tf, 1), "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(pk_tf / FP8_PEAK_TFLOPS, 4), "avg_launch_us": round(pk * 1e3, 2),
+                         "flops_per_launch": 2 * Mp * N * K},
             "kernels": pshape,
         }
-        log(f"bench: prefill step {pms:.3f} ms, gate+up GEMM {pk_tf:.0f} TFLOP/s")
+        log(f"bench: prefill step {pms:.3f} ms, kernels {pshape}")
 
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")

@@ -56,11 +56,16 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K) {
 // Bytes of the split-K partials for these sizes (0 when no split).
 int64_t partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
   if (M > jv::kDecodeMaxRows) return 0;
-  const int s = jv::decode_splits(N, K, cus);
+  const int s = jv::decode_plan(M, N, K, cus).splits;
   return s > 1 ? round_up((int64_t)s * M * N * 4, 256) : 0;
 }
 
-int run_gemm(const uint8_t* xq, int64_t ldxq, const float* sx, const uint8_t* w, int64_t ldw, const float* sw,
+// Activation codes for jv_fp8_linear: packed decode layout for M <= 64, row-major above.
+int64_t codes_bytes(int64_t M, int64_t K) {
+  return M <= jv::kDecodeMaxRows ? jv::packed_x_bytes(M, K) : M * K;
+}
+
+int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, const uint8_t* w, int64_t ldw, const float* sw,
              const uint16_t* bias, const float* lora_t, const uint16_t* lora_b, int64_t rank, float lora_scaling, uint16_t* y,
              int64_t ldy, int64_t M, int64_t N, int64_t K, uint8_t* partial_ws, int64_t partial_ws_bytes,
              int32_t* counters, int64_t n_counters, hipStream_t stream) {
@@ -70,10 +75,11 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, const float* sx, const uint8_t* w,
     return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
   jv::Epilogue ep{sx, sw, bias, lora_t, lora_b, lora_scaling, y, ldy};
   if (M <= jv::kDecodeMaxRows) {
-    const int splits = jv::decode_splits(N, K, cus);
+    const jv::DecodePlan plan = jv::decode_plan(M, N, K, cus);
+    const int splits = plan.splits;
     float* partial = nullptr;
     if (splits > 1) {
-      const int64_t tiles = (N + 15) / 16;
+      const int64_t tiles = plan.groups;
       if (!counters || tiles > n_counters)
         return fail(JV_ERR_VALUE, "%lld tiles exceed the %lld tile counters", (long long)tiles, (long long)n_counters);
       const int64_t need = (int64_t)splits * M * N * 4;
@@ -82,7 +88,8 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, const float* sx, const uint8_t* w,
                     (long long)need);
       partial = reinterpret_cast<float*>(partial_ws);
     }
-    return hip_status(jv::gemm_decode(xq, ldxq, w, ldw, (int)M, (int)N, (int)K, splits, partial, counters, ep, (int)rank, stream),
+    return hip_status(jv::gemm_decode(xq, ldxq, packed_x, w, ldw, (int)M, (int)N, (int)K, plan, partial, counters, ep, (int)rank,
+                                      stream),
                       "fp8 decode GEMM launch");
   }
   const jv::PrefillTile tile = jv::prefill_tile(M, N, cus);
@@ -113,7 +120,7 @@ int jv_fp8_quantize_rows_bf16(const void* x, int64_t ldx, int64_t rows, int64_t 
   if (!aligned16(x) || (ldx * 2) % 16 || !aligned16(codes) || ldc % 16)
     return fail(JV_ERR_VALUE, "quantize_rows needs 16-byte aligned rows");
   return hip_status(jv::quant_rows_bf16((const uint16_t*)x, ldx, rows, (int)cols, (uint8_t*)codes, ldc, scales, nullptr, 0,
-                                        nullptr, (hipStream_t)stream),
+                                        nullptr, false, (hipStream_t)stream),
                     "quantize_rows launch");
 }
 
@@ -137,7 +144,7 @@ int64_t jv_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
 int64_t jv_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t lora_rank) {
   const int cus = cu_count_of(-1);
   if (cus <= 0) return -1;
-  return round_up(M * K, 256) + round_up(M * 4, 256) + round_up(M * lora_rank * 4, 256) + partial_bytes(M, N, K, cus);
+  return round_up(codes_bytes(M, K), 256) + round_up(M * 4, 256) + round_up(M * lora_rank * 4, 256) + partial_bytes(M, N, K, cus);
 }
 
 int jv_fp8_gemm(const void* xq, int64_t ldxq, const float* x_scale, const void* w, int64_t ldw, const float* w_scale,
@@ -149,7 +156,7 @@ int jv_fp8_gemm(const void* xq, int64_t ldxq, const float* x_scale, const void* 
   if (M == 0) return JV_OK;
   if (!aligned16(xq) || ldxq % 16 || !aligned16(w) || ldw % 16)
     return fail(JV_ERR_VALUE, "the fp8 GEMM needs 16-byte aligned operand rows");
-  return run_gemm((const uint8_t*)xq, ldxq, x_scale, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t,
+  return run_gemm((const uint8_t*)xq, ldxq, false, x_scale, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t,
                   (const uint16_t*)lora_b, lora_rank, lora_scaling, (uint16_t*)y, ldy, M, N, K, (uint8_t*)workspace,
                   workspace_bytes, tile_counters, n_counters, (hipStream_t)stream);
 }
@@ -171,7 +178,8 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
     return fail(JV_ERR_VALUE, "workspace needs %lld bytes, 256-byte aligned", (long long)need);
   uint8_t* ws = (uint8_t*)workspace;
   uint8_t* codes = ws;
-  ws += round_up(M * K, 256);
+  const bool packed = M <= jv::kDecodeMaxRows;
+  ws += round_up(codes_bytes(M, K), 256);
   float* sx = (float*)ws;
   ws += round_up(M * 4, 256);
   float* lora_t = lora_rank ? (float*)ws : nullptr;
@@ -179,10 +187,10 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
   const int64_t rest = workspace_bytes - (ws - (uint8_t*)workspace);
   hipStream_t s = (hipStream_t)stream;
   if (int rc = hip_status(jv::quant_rows_bf16((const uint16_t*)x, ldx, M, (int)K, codes, K, sx, (const uint16_t*)lora_a,
-                                              (int)lora_rank, lora_t, s),
+                                              (int)lora_rank, lora_t, packed, s),
                           "activation quantization launch"))
     return rc;
-  return run_gemm(codes, K, sx, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t, (const uint16_t*)lora_b,
+  return run_gemm(codes, K, packed, sx, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t, (const uint16_t*)lora_b,
                   lora_rank, lora_scaling, (uint16_t*)y, ldy, M, N, K, ws, rest, tile_counters, n_counters, s);
 }
 
@@ -203,12 +211,14 @@ int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_
 }
 
 int jv_fp8_split_for(int64_t M, int64_t N, int64_t K, int cu_count) {
-  if (M > jv::kDecodeMaxRows || K <= 0 || N <= 0) return 1;
-  return jv::decode_splits(N, K, cu_count);
+  if (M > jv::kDecodeMaxRows || K <= 0 || N <= 0 || cu_count <= 0) return 1;
+  return jv::decode_plan(M, N, K, cu_count).splits;
 }
 
 int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count) {
-  return jv_fp8_split_for(M, N, K, cu_count) > 1 ? (N + 15) / 16 : 0;
+  if (M > jv::kDecodeMaxRows || K <= 0 || N <= 0 || cu_count <= 0) return 0;
+  const jv::DecodePlan p = jv::decode_plan(M, N, K, cu_count);
+  return p.splits > 1 ? p.groups : 0;
 }
 
 }  // extern "C"

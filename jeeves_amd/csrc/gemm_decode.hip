@@ -5,31 +5,36 @@
 //   * weights are the MFMA "A" side (16 output channels x 128 k per
 //     v_mfma_f32_16x16x128_f8f6f4) and tokens the "B" side, up to 4 token
 //     tiles of 16 (swap-AB, as inference/fp8.py:69 does);
-//   * each lane streams 32 contiguous bytes of one weight row per 128-k step
-//     straight from HBM into the MFMA operand registers (no LDS round trip),
-//     UNROLL steps in flight per wave;
-//   * a workgroup owns 16 weight rows; its WAVES waves split the workgroup's
-//     k range and are summed through LDS in wave order; when there are fewer
-//     16-row tiles than CUs, workgroups also split K (grid.y) and the last
-//     workgroup to finish a tile sums the fp32 partials in split order, then
-//     resets the tile's counter -- one launch, deterministic, capture-safe.
+//   * each lane streams 32 bytes of one weight row per 128-k step straight
+//     from HBM into MFMA operand registers (no LDS round trip), UNROLL steps
+//     in flight per wave; a wave owns RT 16-row tiles so each activation
+//     fragment it loads feeds RT MFMAs;
+//   * activation codes come either row-major [M,K] or, from the fused
+//     quantizer, pre-packed in MFMA B-fragment order (packed_x_offset), so a
+//     wave's activation load is one contiguous 1 KB per instruction;
+//   * the WAVES waves of a workgroup split the workgroup's k range and are
+//     summed through LDS in wave order; for very small N, workgroups also
+//     split K (grid.y): partials go to memory with device-coherent stores, and
+//     the last workgroup of a tile (device-scope counter) sums them in split
+//     order and resets the counter -- one launch, deterministic, no cache
+//     flushes, capture-safe.
 #include "epilogue.h"
 #include "kernels.h"
 
 namespace jv {
 
-template <int MT, int WAVES, int UNROLL, int RANK>
+template <int MT, int RT, int WAVES, int UNROLL, bool PACKX, int RANK>
 __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* __restrict__ xq, int64_t ldxq,
                                                                  const uint8_t* __restrict__ w, int64_t ldw, int M, int N,
                                                                  int K, int splits, float* __restrict__ partial,
                                                                  int* __restrict__ counters, Epilogue ep) {
-  __shared__ f32x4 red[WAVES][MT][64];
+  __shared__ f32x4 red[WAVES][RT * MT][64];
   __shared__ int is_last;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int tile = blockIdx.x;
+  const int group = blockIdx.x;
   const int split = blockIdx.y;
-  const int n0 = tile * 16;
+  const int n0 = group * 16 * RT;
 
   const int ksteps = K >> 7;
   const int slices = splits * WAVES;
@@ -39,139 +44,161 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
 
   const int li = lane & 15;
   const int lk = (lane >> 4) * 32;
-  const uint8_t* wp = w + (int64_t)min(n0 + li, N - 1) * ldw + lk;
+  const uint8_t* wp[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) wp[rt] = w + (int64_t)min(n0 + rt * 16 + li, N - 1) * ldw + lk;
   const uint8_t* xp[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) xp[mt] = xq + (int64_t)min(mt * 16 + li, M - 1) * ldxq + lk;
+  for (int mt = 0; mt < MT; ++mt)
+    xp[mt] = PACKX ? xq + (int64_t)mt * ksteps * 2048 + lane * 16 : xq + (int64_t)min(mt * 16 + li, M - 1) * ldxq + lk;
 
-  f32x4 acc[MT];
+  f32x4 acc[RT][MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  int s = s_begin;
-  for (; s + UNROLL <= s_end; s += UNROLL) {
-    i32x4 wa[UNROLL][2];
+  for (int s = s_begin; s < s_end; s += UNROLL) {
+    i32x4 wa[UNROLL][RT][2];
     i32x4 xa[UNROLL][MT][2];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
+      if (s + u >= s_end) break;
       const int64_t off = (int64_t)(s + u) * 128;
-      wa[u][0] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wp + off));
-      wa[u][1] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wp + off + 16));
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        wa[u][rt][0] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wp[rt] + off));
+        wa[u][rt][1] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wp[rt] + off + 16));
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        xa[u][mt][0] = *reinterpret_cast<const i32x4*>(xp[mt] + off);
-        xa[u][mt][1] = *reinterpret_cast<const i32x4*>(xp[mt] + off + 16);
+        const int64_t xo = PACKX ? (int64_t)(s + u) * 2048 : off;
+        xa[u][mt][0] = *reinterpret_cast<const i32x4*>(xp[mt] + xo);
+        xa[u][mt][1] = *reinterpret_cast<const i32x4*>(xp[mt] + xo + (PACKX ? 1024 : 16));
       }
     }
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      const i32x8 a = cat8(wa[u][0], wa[u][1]);
+      if (s + u >= s_end) break;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma_16x16x128_fp8(a, cat8(xa[u][mt][0], xa[u][mt][1]), acc[mt]);
+      for (int mt = 0; mt < MT; ++mt) {
+        const i32x8 b = cat8(xa[u][mt][0], xa[u][mt][1]);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt][mt] = mfma_16x16x128_fp8(cat8(wa[u][rt][0], wa[u][rt][1]), b, acc[rt][mt]);
+      }
     }
   }
-  for (; s < s_end; ++s) {
-    const int64_t off = (int64_t)s * 128;
-    const i32x8 a = cat8(__builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wp + off)),
-                         __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wp + off + 16)));
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      acc[mt] = mfma_16x16x128_fp8(a,
-                                   cat8(*reinterpret_cast<const i32x4*>(xp[mt] + off),
-                                        *reinterpret_cast<const i32x4*>(xp[mt] + off + 16)),
-                                   acc[mt]);
-  }
 
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[wave][rt * MT + mt][lane] = acc[rt][mt];
   __syncthreads();
 
-  // Output (m_local, n_local) of token tile mt lives in lane m_local + 16*(n_local/4),
+  // Output (m_local, n_local) of tile (rt, mt) lives in lane m_local + 16*(n_local/4),
   // register n_local % 4 (16x16 MFMA layout: row = 4*(lane/16) + reg, col = lane % 16,
   // with rows = weight channels and cols = tokens). Threads walk n fastest so
   // consecutive threads store consecutive channels of one token.
   const float* redf = reinterpret_cast<const float*>(&red[0][0][0]);
-  constexpr int kOut = MT * 256;
-  if (splits == 1) {
-    for (int idx = threadIdx.x; idx < kOut; idx += 64 * WAVES) {
-      const int mt = idx >> 8, e = idx & 255, ml = e >> 4, nl = e & 15;
-      const int src = ((mt * 64) + ml + 16 * (nl >> 2)) * 4 + (nl & 3);
-      float sum = 0.0f;
-#pragma unroll
-      for (int wv = 0; wv < WAVES; ++wv) sum += redf[wv * MT * 256 + src];
-      const int m = mt * 16 + ml, n = n0 + nl;
-      if (m < M && n < N) ep.y[(int64_t)m * ep.ldy + n] = (uint16_t)f32_to_bf16(epilogue_value<RANK>(ep, sum, m, n, ep.sx[m], ep.sw[n]));
-    }
-    return;
-  }
-
+  constexpr int kOut = RT * MT * 256;
   for (int idx = threadIdx.x; idx < kOut; idx += 64 * WAVES) {
-    const int mt = idx >> 8, e = idx & 255, ml = e >> 4, nl = e & 15;
-    const int src = ((mt * 64) + ml + 16 * (nl >> 2)) * 4 + (nl & 3);
+    const int t = idx >> 8, rt = t / MT, mt = t % MT, e = idx & 255, ml = e >> 4, nl = e & 15;
+    const int src = (t * 64 + ml + 16 * (nl >> 2)) * 4 + (nl & 3);
     float sum = 0.0f;
 #pragma unroll
-    for (int wv = 0; wv < WAVES; ++wv) sum += redf[wv * MT * 256 + src];
-    const int m = mt * 16 + ml, n = n0 + nl;
-    if (m < M && n < N) partial[((int64_t)split * M + m) * N + n] = sum;
+    for (int wv = 0; wv < WAVES; ++wv) sum += redf[wv * RT * MT * 256 + src];
+    const int m = mt * 16 + ml, n = n0 + rt * 16 + nl;
+    if (m < M && n < N) {
+      if (splits == 1)
+        ep.y[(int64_t)m * ep.ldy + n] = (uint16_t)f32_to_bf16(epilogue_value<RANK>(ep, sum, m, n, ep.sx[m], ep.sw[n]));
+      else  // device-coherent store: visible to the reducing workgroup without a cache flush
+        __hip_atomic_store(partial + ((int64_t)split * M + m) * N + n, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
-  // Publish the partial (release at agent scope), then count this split in.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  if (splits == 1) return;
+
+  // Every partial store of this workgroup has completed (s_waitcnt) before
+  // its count is added; the workgroup that sees count splits-1 reads all
+  // partials with device-coherent loads.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(counters + tile, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = prev == splits - 1;
-  }
+  if (threadIdx.x == 0)
+    is_last = __hip_atomic_fetch_add(counters + group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
   __syncthreads();
   if (!is_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   for (int idx = threadIdx.x; idx < kOut; idx += 64 * WAVES) {
-    const int mt = idx >> 8, e = idx & 255, ml = e >> 4, nl = e & 15;
-    const int m = mt * 16 + ml, n = n0 + nl;
+    const int t = idx >> 8, rt = t / MT, mt = t % MT, e = idx & 255, ml = e >> 4, nl = e & 15;
+    const int m = mt * 16 + ml, n = n0 + rt * 16 + nl;
     if (m < M && n < N) {
       float sum = 0.0f;
-      for (int sp = 0; sp < splits; ++sp) sum += partial[((int64_t)sp * M + m) * N + n];
+      for (int sp = 0; sp < splits; ++sp)
+        sum += __hip_atomic_load(partial + ((int64_t)sp * M + m) * N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       ep.y[(int64_t)m * ep.ldy + n] = (uint16_t)f32_to_bf16(epilogue_value<RANK>(ep, sum, m, n, ep.sx[m], ep.sw[n]));
     }
   }
-  if (threadIdx.x == 0) __hip_atomic_store(counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(counters + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-int decode_splits(int64_t N, int64_t K, int cu_count) {
+DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count) {
+  DecodePlan p;
   const int64_t tiles = (N + 15) / 16;
-  const int64_t ksteps = K / 128;
-  if (tiles >= cu_count) return 1;
-  int64_t s = (cu_count + tiles - 1) / tiles;
-  const int64_t max_s = ksteps / kDecodeWaves;
-  if (s > max_s) s = max_s;
-  if (s > 16) s = 16;
-  return s < 1 ? 1 : (int)s;
-}
-
-template <int MT, int RANK>
-static void launch_decode_mt(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
-                             int splits, float* partial, int* counters, const Epilogue& ep, hipStream_t stream) {
-  const dim3 grid((unsigned)((N + 15) / 16), (unsigned)splits), block(64 * kDecodeWaves);
-  gemm_decode_kernel<MT, kDecodeWaves, kDecodeUnroll, RANK>
-      <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, splits, partial, counters, ep);
-}
-
-hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K, int splits,
-                       float* partial, int* counters, const Epilogue& ep, int rank, hipStream_t stream) {
-  const int mt = (M + 15) / 16;
-  if (mt < 1 || mt > 4 || (rank != 0 && rank != 16)) return hipErrorInvalidValue;
-#define JV_DECODE_CASE(MT_)                                                                          \
-  if (mt == MT_) {                                                                                   \
-    if (rank == 16)                                                                                  \
-      launch_decode_mt<MT_, 16>(xq, ldxq, w, ldw, M, N, K, splits, partial, counters, ep, stream);   \
-    else                                                                                             \
-      launch_decode_mt<MT_, 0>(xq, ldxq, w, ldw, M, N, K, splits, partial, counters, ep, stream);    \
+  p.rt = tiles >= 4 * (int64_t)cu_count ? 2 : 1;
+  const int64_t groups = (tiles + p.rt - 1) / p.rt;
+  p.groups = (int)groups;
+  // Splitting K across workgroups only pays when the tiles cannot occupy an
+  // eighth of the CUs: below that the launch is latency-bound either way.
+  p.splits = 1;
+  if (groups * 8 < cu_count) {
+    int64_t s = (cu_count + groups - 1) / groups;
+    const int64_t max_s = (K / 128) / kDecodeWaves;
+    if (s > max_s) s = max_s;
+    if (s > 16) s = 16;
+    p.splits = s < 1 ? 1 : (int)s;
   }
-  JV_DECODE_CASE(1)
-  JV_DECODE_CASE(2)
-  JV_DECODE_CASE(3)
-  JV_DECODE_CASE(4)
-#undef JV_DECODE_CASE
+  (void)M;
+  return p;
+}
+
+template <int MT, int RT, int U, bool PACKX, int RANK>
+static void launch_decode(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                          const DecodePlan& p, float* partial, int* counters, const Epilogue& ep, hipStream_t stream) {
+  const dim3 grid((unsigned)p.groups, (unsigned)p.splits), block(64 * kDecodeWaves);
+  gemm_decode_kernel<MT, RT, kDecodeWaves, U, PACKX, RANK>
+      <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, p.splits, partial, counters, ep);
+}
+
+template <int MT, bool PACKX, int RANK>
+static void launch_decode_rt(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                             const DecodePlan& p, float* partial, int* counters, const Epilogue& ep, hipStream_t stream) {
+  if (p.rt == 2)
+    launch_decode<MT, 2, 4, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+  else
+    launch_decode<MT, 1, 8, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+}
+
+template <bool PACKX, int RANK>
+static hipError_t launch_decode_mt(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                                   const DecodePlan& p, float* partial, int* counters, const Epilogue& ep,
+                                   hipStream_t stream) {
+  switch ((M + 15) / 16) {
+    case 1: launch_decode_rt<1, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
+    case 2: launch_decode_rt<2, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
+    case 3: launch_decode_rt<3, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
+    case 4: launch_decode_rt<4, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
+}
+
+hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, bool packed_x, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                       const DecodePlan& plan, float* partial, int* counters, const Epilogue& ep, int rank,
+                       hipStream_t stream) {
+  if (M < 1 || M > kDecodeMaxRows || (rank != 0 && rank != 16)) return hipErrorInvalidValue;
+  if (packed_x)
+    return rank == 16 ? launch_decode_mt<true, 16>(xq, ldxq, w, ldw, M, N, K, plan, partial, counters, ep, stream)
+                      : launch_decode_mt<true, 0>(xq, ldxq, w, ldw, M, N, K, plan, partial, counters, ep, stream);
+  return rank == 16 ? launch_decode_mt<false, 16>(xq, ldxq, w, ldw, M, N, K, plan, partial, counters, ep, stream)
+                    : launch_decode_mt<false, 0>(xq, ldxq, w, ldw, M, N, K, plan, partial, counters, ep, stream);
 }
 
 }  // namespace jv

@@ -11,24 +11,44 @@ namespace jv {
 // Decode regime: M <= kDecodeMaxRows tokens.
 constexpr int kDecodeMaxRows = 64;
 constexpr int kDecodeWaves = 4;
-constexpr int kDecodeUnroll = 4;
+
+struct DecodePlan {
+  int rt;      // 16-row tiles per wave
+  int groups;  // workgroups along N
+  int splits;  // workgroups along K
+};
 
 struct PrefillTile {
   int bm, bn;
 };
 
+// Byte offset of activation code (m, k) in the packed decode layout: for
+// token tile mt = m/16 and 128-k step s, two 1 KB halves, each holding 16
+// bytes per lane in MFMA B-fragment order (lane = m%16 + 16*((k%128)/32),
+// half = (k%32)/16). Rows are padded to a multiple of 16 tokens.
+__host__ __device__ inline int64_t packed_x_offset(int m, int k, int ksteps) {
+  const int mt = m >> 4, s = k >> 7, kk = k & 127;
+  const int lane = (m & 15) + 16 * (kk >> 5), half = (kk >> 4) & 1;
+  return ((((int64_t)mt * ksteps + s) * 2 + half) << 10) + lane * 16 + (kk & 15);
+}
+
+inline int64_t packed_x_bytes(int64_t M, int64_t K) { return (M + 15) / 16 * 16 * K; }
+
 int quant_chunks(int K);
+// packed: write codes in the packed decode layout (codes sized
+// packed_x_bytes(M, K), ldc ignored; the padding rows get zero codes).
 hipError_t quant_rows_bf16(const uint16_t* x, int64_t ldx, int64_t M, int K, uint8_t* codes, int64_t ldc, float* scales,
-                           const uint16_t* lora_a, int rank, float* lora_t, hipStream_t stream);
+                           const uint16_t* lora_a, int rank, float* lora_t, bool packed, hipStream_t stream);
 hipError_t quant_swiglu_bf16(const uint16_t* gate, int64_t ldg, const uint16_t* up, int64_t ldu, int64_t M, int K,
                              uint8_t* codes, int64_t ldc, float* scales, uint16_t* h_out, int64_t ldh,
                              const uint16_t* lora_a, int rank, float* lora_t, hipStream_t stream);
 hipError_t quant_rows_f32(const float* x, int64_t ldx, int64_t M, int K, uint8_t* codes, int64_t ldc, float* scales,
                           hipStream_t stream);
 
-int decode_splits(int64_t N, int64_t K, int cu_count);
-hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K, int splits,
-                       float* partial, int* counters, const Epilogue& ep, int rank, hipStream_t stream);
+DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count);
+hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, bool packed_x, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                       const DecodePlan& plan, float* partial, int* counters, const Epilogue& ep, int rank,
+                       hipStream_t stream);
 
 PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count);
 hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,

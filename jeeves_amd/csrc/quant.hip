@@ -17,6 +17,7 @@
 //   * RANK > 0: also emits the LoRA down-projection t[m,r] = sum_k x[m,k] A[r,k]
 //     (model/lora.py:128-131) in fp32 from the same registers.
 #include "fp8_common.h"
+#include "kernels.h"
 
 namespace jv {
 
@@ -25,7 +26,7 @@ constexpr int kQuantThreads = 256;
 // silu in fp32 rounded to bf16, times up, rounded to bf16.
 __device__ __forceinline__ uint32_t swiglu_bf16(uint32_t g16, uint32_t u16) {
   const float g = bf16_to_f32(g16);
-  const float s = g / (1.0f + __expf(-g));
+  const float s = g / (1.0f + expf(-g));
   const float sb = bf16_to_f32(f32_to_bf16(s));
   return f32_to_bf16(sb * bf16_to_f32(u16));
 }
@@ -99,9 +100,11 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
 }
 
 // NC: chunks of 8 elements per thread kept in registers (K <= NC * 2048).
-template <int NC, bool SWIGLU, int RANK>
+// PACKED: codes go to the packed decode layout (packed_x_offset); the grid
+// then also covers the padding rows M..16*ceil(M/16)-1, which get zero codes.
+template <int NC, bool SWIGLU, int RANK, bool PACKED>
 __global__ __launch_bounds__(kQuantThreads) void quant_rows_bf16_kernel(
-    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ up, int64_t ldu, int K,
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ up, int64_t ldu, int K, int M,
     uint8_t* __restrict__ codes, int64_t ldc, float* __restrict__ scales, uint16_t* __restrict__ h_out, int64_t ldh,
     const uint16_t* __restrict__ lora_a, float* __restrict__ lora_t) {
   __shared__ uint32_t red[4];
@@ -109,6 +112,11 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_bf16_kernel(
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int nchunks = K >> 3;
+  if (PACKED && row >= M) {
+    for (int c = tid; c < nchunks; c += kQuantThreads)
+      *reinterpret_cast<uint2*>(codes + packed_x_offset((int)row, c * 8, K >> 7)) = uint2{0u, 0u};
+    return;
+  }
   const uint16_t* xr = x + row * ldx;
   uint4 v[NC];
   uint32_t am = 0;
@@ -143,11 +151,14 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_bf16_kernel(
   if (tid == 0) scales[row] = scale;
   const bool fast = amax_bits < 0x7F80u;  // finite row: scale finite and > 0
   const float r = 1.0f / scale;
-  uint8_t* cr = codes + row * ldc;
+  uint8_t* cr = codes + (PACKED ? 0 : row * ldc);
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int c = tid + i * kQuantThreads;
-    if (c < nchunks) *reinterpret_cast<uint2*>(cr + (int64_t)c * 8) = encode8(v[i], scale, r, fast);
+    if (c < nchunks) {
+      const int64_t off = PACKED ? packed_x_offset((int)row, c * 8, K >> 7) : (int64_t)c * 8;
+      *reinterpret_cast<uint2*>(cr + off) = encode8(v[i], scale, r, fast);
+    }
   }
   if constexpr (RANK > 0) {
     const int lane = tid & 63, wave = tid >> 6;
@@ -227,15 +238,15 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_f32_kernel(const flo
   }
 }
 
-template <bool SWIGLU, int RANK>
+template <bool SWIGLU, int RANK, bool PACKED = false>
 static hipError_t launch_rows(int NC, const uint16_t* x, int64_t ldx, const uint16_t* up, int64_t ldu, int64_t M, int K,
                               uint8_t* codes, int64_t ldc, float* scales, uint16_t* h_out, int64_t ldh,
                               const uint16_t* lora_a, float* lora_t, hipStream_t stream) {
-  const dim3 grid((unsigned)M), block(kQuantThreads);
+  const dim3 grid((unsigned)(PACKED ? (M + 15) / 16 * 16 : M)), block(kQuantThreads);
 #define JV_QUANT_CASE(n)                                                                                              \
   case n:                                                                                                             \
-    quant_rows_bf16_kernel<n, SWIGLU, RANK>                                                                          \
-        <<<grid, block, 0, stream>>>(x, ldx, up, ldu, K, codes, ldc, scales, h_out, ldh, lora_a, lora_t);           \
+    quant_rows_bf16_kernel<n, SWIGLU, RANK, PACKED>                                                                  \
+        <<<grid, block, 0, stream>>>(x, ldx, up, ldu, K, (int)M, codes, ldc, scales, h_out, ldh, lora_a, lora_t);   \
     break;
   switch (NC) {
     JV_QUANT_CASE(1)
@@ -262,9 +273,17 @@ int quant_chunks(int K) {
 }
 
 hipError_t quant_rows_bf16(const uint16_t* x, int64_t ldx, int64_t M, int K, uint8_t* codes, int64_t ldc, float* scales,
-                           const uint16_t* lora_a, int rank, float* lora_t, hipStream_t stream) {
+                           const uint16_t* lora_a, int rank, float* lora_t, bool packed, hipStream_t stream) {
   if (M == 0) return hipSuccess;
   const int nc = quant_chunks(K);
+  if (packed) {
+    if (nc == 0 || M > kDecodeMaxRows || (K & 127)) return hipErrorInvalidValue;
+    if (rank == 16)
+      return launch_rows<false, 16, true>(nc, x, ldx, nullptr, 0, M, K, codes, 0, scales, nullptr, 0, lora_a, lora_t, stream);
+    if (rank == 0)
+      return launch_rows<false, 0, true>(nc, x, ldx, nullptr, 0, M, K, codes, 0, scales, nullptr, 0, nullptr, nullptr, stream);
+    return hipErrorInvalidValue;
+  }
   if (rank == 0) {
     if (nc == 0) {
       quant_rows_bf16_long_kernel<<<dim3((unsigned)M), dim3(kQuantThreads), 0, stream>>>(x, ldx, K, codes, ldc, scales);

@@ -70,12 +70,15 @@ def test_error_mapping():
 
 def test_split_for_is_pure_host_logic(product_lib):
     L = product_lib
-    # 256 CUs: q/o (256 tiles of 16 rows) need no split; k/v (64 tiles) split 4 ways
+    # 256 CUs: every 9B projection has enough 16-row tiles (k/v: 64) to skip split-K;
+    # only N < 512 (fewer than 32 tiles) splits K across workgroups
     assert L.jv_fp8_split_for(16, 4096, 4096, 256) == 1
-    assert L.jv_fp8_split_for(16, 1024, 4096, 256) == 4
+    assert L.jv_fp8_split_for(16, 1024, 4096, 256) == 1
     assert L.jv_fp8_split_for(16, 24576, 4096, 256) == 1
-    assert L.jv_fp8_split_for(2048, 1024, 4096, 256) == 1  # prefill never splits
-    assert L.jv_fp8_counters_needed(16, 1024, 4096, 256) == 64
+    assert L.jv_fp8_split_for(16, 256, 4096, 256) == 8   # 16 tiles, capped at K/128/4
+    assert L.jv_fp8_split_for(16, 128, 12288, 256) == 16  # 8 tiles, capped at 16
+    assert L.jv_fp8_split_for(2048, 128, 4096, 256) == 1  # prefill never splits
+    assert L.jv_fp8_counters_needed(16, 256, 4096, 256) == 16
     assert L.jv_fp8_counters_needed(16, 4096, 4096, 256) == 0
 
 

@@ -81,6 +81,26 @@ def test_decode_workload_shapes(name, M):
     check(fp8_matmul(x, wq, sw), x, wq, sw)
 
 
+@pytest.mark.parametrize("N,K", [(256, 4096), (128, 12288), (144, 1024)])
+@pytest.mark.parametrize("M", [1, 16, 33, 64])
+def test_split_k_decode_path(N, K, M):
+    """Narrow weights (N < 512) split K across workgroups; the last workgroup of
+    each tile sums the partials in split order and leaves the counters zero."""
+    from jeeves_amd import TILE_COUNTERS
+    from jeeves_amd.device import sm_count
+
+    assert _lib.lib().jv_fp8_split_for(M, N, K, sm_count(torch.device("cuda"))) > 1
+    x = synthetic.activations_heavy_tail(M, K, 70 + M)
+    w = synthetic.weight(N, K, 71)
+    wq, sw = quantize_rows(w.cuda())
+    x = x.cuda()
+    y = fp8_matmul(x, wq, sw)
+    check(y, x, wq, sw)
+    assert torch.equal(y, fp8_matmul(x, wq, sw)), "split-K result is not deterministic"
+    torch.cuda.synchronize()
+    assert all(int(c.abs().sum()) == 0 for c in TILE_COUNTERS.values())
+
+
 @pytest.mark.parametrize("name", list(synthetic.SHAPES))
 @pytest.mark.parametrize("M", [512, 2048])
 def test_prefill_workload_shapes(name, M):
