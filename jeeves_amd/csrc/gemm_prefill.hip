@@ -5,22 +5,43 @@
 //   * both operands are K-contiguous e4m3 (activation codes [M,K] from the
 //     quantizer, weight codes [N,K]) and feed v_mfma_f32_32x32x64_f8f6f4
 //     directly: no fp8 -> fp16 conversion in the main loop;
-//   * a BM x BN output tile per 256-thread workgroup (2 x 2 waves, each wave a
-//     (BM/2) x (BN/2) tile of 32x32 MFMA blocks, fp32 accumulators);
+//   * a BM (tokens) x BN (channels) output tile per workgroup of WGM x WGN
+//     waves; each wave owns a (BM/WGM) x (BN/WGN) sub-tile of 32x32 MFMA
+//     blocks with fp32 accumulators. With 8 waves two waves share each SIMD,
+//     so one wave's LDS reads overlap the other's MFMAs;
+//   * weights are the MFMA A operand and tokens the B operand, so each lane
+//     ends with 4 consecutive channels of one token per register quad and the
+//     epilogue stores 8 bytes per lane;
 //   * K advances 128 bytes per stage; each stage's A and B rows are copied
 //     global -> LDS with global_load_lds_dwordx4 (no VGPR staging), double
 //     buffered so the next stage's copy overlaps this stage's MFMAs;
 //   * LDS rows are 128 B with the 16-byte chunk index XOR-swizzled by (row & 7),
 //     so the 8 lanes of each ds_read_b128 phase hit 8 distinct bank groups;
+//   * workgroups are renumbered so that each XCD (the hardware hands
+//     consecutive workgroups to the 8 XCDs in turn) works on a contiguous
+//     range of tiles: a weight tile is fetched into one XCD's L2, not eight;
 //   * fused epilogue acc * sx[m] * sw[n] (+ bias, + LoRA) -> bf16.
 #include "epilogue.h"
 #include "kernels.h"
 
 namespace jv {
 
-constexpr int kBK = 128;
+constexpr int kXcds = 8;
 
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmem_below() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier without the memory fence __syncthreads() carries (the
+// fence makes the compiler drain every outstanding load first, which would
+// empty the copy pipeline). Callers order their own memory: each wave waits
+// for its global -> LDS copies with wait_vmem_below before the barrier, and
+// has consumed its earlier LDS reads (their MFMAs issued) before reaching it.
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
 // Copy 16 bytes per lane from global to LDS: lane i's bytes land at dst + 16 * i.
 __device__ __forceinline__ void load_lds16(const uint8_t* src, uint8_t* dst_wave_base) {
@@ -31,149 +52,293 @@ __device__ __forceinline__ void load_lds16(const uint8_t* src, uint8_t* dst_wave
 
 __device__ __forceinline__ i32x4 lds_read16(const uint8_t* p) { return *reinterpret_cast<const i32x4*>(p); }
 
-template <int BM, int BN, int RANK>
-__global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __restrict__ xq, int64_t ldx,
-                                                           const uint8_t* __restrict__ w, int64_t ldw, int M, int N, int K,
-                                                           int tiles_m, int tiles_n, Epilogue ep) {
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int STAGE = (BM + BN) * kBK;
-  constexpr int LOADS = (BM + BN) / 32;  // 1 KB wave-loads per wave per stage
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
+// LDS tile rows are BK bytes = BK/16 chunks of 16 B. gfx950 serves a
+// ds_read_b128 16 lanes at a time from 64 four-byte banks (256 B), so the 16
+// rows a fragment read touches at one logical chunk must fall in 16 distinct
+// 16-byte bank groups. Row r's bank groups start at (r * BK/16) mod 16, which
+// repeats every P = 256/BK rows; XOR-ing the chunk index with (r / P) mod
+// (BK/16) separates the rows that share a start.
+template <int BK>
+__device__ __forceinline__ int swizzle(int row) {
+  constexpr int CH = BK / 16, P = 256 / BK;
+  return (row / P) % CH;
+}
 
-  // Tile order: groups of 8 M-tiles walk N together, so concurrently resident
-  // workgroups share A rows and B rows in L2.
-  const int pid = blockIdx.x;
-  constexpr int GROUP = 8;
-  const int per_group = GROUP * tiles_n;
-  const int group = pid / per_group;
-  const int first_m = group * GROUP;
-  const int gsize = min(tiles_m - first_m, GROUP);
-  const int tile_m = first_m + (pid % per_group) % gsize;
-  const int tile_n = (pid % per_group) / gsize;
+// Workgroup -> output tile. Workgroup ids are first regrouped so that XCD x
+// (ids x, x+8, x+16, ...) receives one contiguous range of logical tiles;
+// logical tiles then run in groups of `group_m` M-tiles that walk N together.
+__device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int group_m, int& tile_m, int& tile_n) {
+  const int total = tiles_m * tiles_n;
+  const int base = total / kXcds, rem = total % kXcds;
+  const int xcd = pid % kXcds, local = pid / kXcds;
+  const int q = (xcd < rem ? xcd * (base + 1) : rem * (base + 1) + (xcd - rem) * base) + local;
+  const int per_group = group_m * tiles_n;
+  const int first_m = (q / per_group) * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int r = q % per_group;
+  tile_m = first_m + r % gsize;
+  tile_n = r / gsize;
+}
+
+template <int BM, int BN, int WGM, int WGN, int BK, int STAGES, int RANK>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint8_t* __restrict__ xq, int64_t ldx,
+                                                                      const uint8_t* __restrict__ w, int64_t ldw, int M,
+                                                                      int N, int K, int tiles_m, int tiles_n, int group_m,
+                                                                      Epilogue ep) {
+  constexpr int NW = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;  // wave sub-tile: tokens x channels
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int CH = BK / 16;                  // 16-byte chunks per LDS row
+  constexpr int RPL = 1024 / BK;               // rows per 1 KB wave-load
+  constexpr int ROWS = BM + BN;                // stacked LDS rows: tokens, then channels
+  constexpr int STAGE = ROWS * BK;
+  constexpr int LOADS = ROWS / RPL / NW;       // wave-loads per wave per stage
+  constexpr int SUB = BK / 64;                 // 64-deep MFMA steps per stage
+  static_assert(BK == 64 || BK == 128, "stage depth");
+  static_assert(ROWS % (RPL * NW) == 0 && TM >= 1 && TN >= 1, "tile does not divide among the waves");
+  static_assert(STAGES >= 3 && (STAGES - 2) * LOADS < 64, "pipeline depth");
+  constexpr int OUT_CH = BN * 2 / 16;          // 16-byte chunks per output tile row
+  constexpr int LDS_BYTES = STAGES * STAGE > BM * BN * 2 ? STAGES * STAGE : BM * BN * 2;
+  static_assert(OUT_CH <= 32 && (OUT_CH & (OUT_CH - 1)) == 0, "output tile width");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+  __shared__ __attribute__((aligned(256))) float scale_lds[BM + BN];  // sx of the tile's tokens, then sw of its channels
+
+  int tile_m, tile_n;
+  tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tile_m, tile_n);
   const int m0 = tile_m * BM, n0 = tile_n * BN;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
 
-  // Global -> LDS assignment. Wave-load g (g = i*4 + wave) fills LDS bytes
-  // [g*1024, g*1024 + 1024) of a stage: rows 8g .. 8g+7 of the stacked
-  // (A rows, then B rows) tile. Lane l writes row 8g + l/8, physical chunk
-  // l%8, which holds logical chunk (l%8) ^ (row & 7) = (l%8) ^ (l/8).
-  const int lrow = lane >> 3;
-  const int lchunk = (lane & 7) ^ lrow;
-  uint32_t src_off[LOADS];
-  bool src_is_a[LOADS];
+  // Global -> LDS assignment. Wave-load g (g = i*NW + wave) fills LDS bytes
+  // [g*1024, g*1024 + 1024) of a stage: stacked rows RPL*g .. RPL*g + RPL-1.
+  // Lane l writes row RPL*g + l/CH at physical chunk l%CH, which holds logical
+  // chunk (l%CH) ^ swizzle(row). Rows past M or N re-read the last valid row;
+  // their products land in outputs that are never stored.
+  const uint8_t* src[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
-    const int r = (i * 4 + wave) * 8 + lrow;
-    if (r < BM) {
-      src_is_a[i] = true;
-      src_off[i] = (uint32_t)((int64_t)min(m0 + r, M - 1) * ldx) + lchunk * 16;
-    } else {
-      src_is_a[i] = false;
-      src_off[i] = (uint32_t)((int64_t)min(n0 + r - BM, N - 1) * ldw) + lchunk * 16;
-    }
+    const int r = (i * NW + wave) * RPL + lane / CH;
+    const int chunk = (lane % CH) ^ swizzle<BK>(r);
+    src[i] = r < BM ? xq + (int64_t)min(m0 + r, M - 1) * ldx + chunk * 16
+                    : w + (int64_t)min(n0 + r - BM, N - 1) * ldw + chunk * 16;
   }
 
-  auto issue_stage = [&](int kt, int buf) {
-    uint8_t* base = lds + buf * STAGE;
-    const int64_t k0 = (int64_t)kt * kBK;
+  auto issue_stage = [&](int kt) {
+    uint8_t* base = lds + (kt % STAGES) * STAGE;
+    const int64_t k0 = (int64_t)kt * BK;
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const uint8_t* src = (src_is_a[i] ? xq : w) + src_off[i] + k0;
-      load_lds16(src, base + (i * 4 + wave) * 1024);
+    for (int i = 0; i < LOADS; ++i) load_lds16(src[i] + k0, base + (i * NW + wave) * 1024);
+  };
+
+  f32x16 acc[TN][TM];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
+
+  // Fragment addressing: lane l reads row (l % 32) of a 32-row block, logical
+  // chunks 4s + 2(l/32) and 4s + 2(l/32) + 1 for 64-deep step s of the stage.
+  const int frow = lane & 31;
+  const int fhalf = (lane >> 5) * 2;
+  int arow[TN], brow[TM];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) arow[j] = BM + wn * WN + j * 32 + frow;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) brow[i] = wm * WM + i * 32 + frow;
+
+  // The tile's token and channel scales go to LDS by DMA before the operand
+  // stages (vector-memory loads complete in order, so the first stage wait
+  // covers them), out of the epilogue's critical path.
+  for (int t = wave * 64; t < BM + BN; t += NW * 64) {
+    const int r = t + lane;
+    const float* sp = r < BM ? ep.sx + min(m0 + r, M - 1) : ep.sw + min(n0 + r - BM, N - 1);
+    typedef __attribute__((address_space(3))) void lds_void;
+    typedef __attribute__((address_space(1))) void global_void;
+    __builtin_amdgcn_global_load_lds((global_void*)sp, (lds_void*)(scale_lds + t), 4, 0, 0);
+  }
+
+  const int KT = K / BK;
+  // Two fragment sets: while the MFMAs of 64-deep step u run on one set, the
+  // LDS reads of step u+1 fill the other.
+  i32x8 fa[2][TN], fb[2][TM];
+  auto load_frags = [&](int kt, int s, i32x8 (&a)[TN], i32x8 (&b)[TM]) {
+    const uint8_t* base = lds + (kt % STAGES) * STAGE;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int r = arow[j], sw = swizzle<BK>(r);
+      a[j] = cat8(lds_read16(base + r * BK + ((4 * s + fhalf) ^ sw) * 16),
+                  lds_read16(base + r * BK + ((4 * s + fhalf + 1) ^ sw) * 16));
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = brow[i], sw = swizzle<BK>(r);
+      b[i] = cat8(lds_read16(base + r * BK + ((4 * s + fhalf) ^ sw) * 16),
+                  lds_read16(base + r * BK + ((4 * s + fhalf + 1) ^ sw) * 16));
     }
   };
 
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  // Stage kt+1 has landed (for every wave, after the barrier) once at most
+  // min(STAGES-3, KT-2-kt) later stages of this wave's copies are in flight.
+  auto wait_stage_after = [&](int kt) {
+    const int later = min(STAGES - 3, KT - 2 - kt);
+    if (STAGES > 3 && later >= STAGES - 3) wait_vmem_below<(STAGES > 3 ? (STAGES - 3) * LOADS : 0)>();
+    else if (STAGES > 4 && later == 1) wait_vmem_below<LOADS>();
+    else wait_vmem_below<0>();
+    barrier_only();
+  };
 
-  // Fragment addressing: lane l reads row (l % 32) of a 32-row block, logical
-  // chunks 4s + 2(l/32) and 4s + 2(l/32) + 1 for k-step s of the stage.
-  const int frow = lane & 31;
-  const int fhalf = (lane >> 5) * 2;
+  const int U = KT * SUB;  // 64-deep steps
+#pragma unroll
+  for (int p = 0; p < STAGES - 1; ++p)
+    if (p < KT) issue_stage(p);
+  // stage 0 landed: at most min(STAGES-2, KT-1) later stages in flight
+  if (STAGES > 3 && KT >= STAGES - 1) wait_vmem_below<(STAGES > 3 ? (STAGES - 2) * LOADS : 0)>();
+  else if (KT >= 2) wait_vmem_below<LOADS>();
+  else wait_vmem_below<0>();
+  barrier_only();
+  load_frags(0, 0, fa[0], fb[0]);
 
-  const int KT = K / kBK;
-  issue_stage(0, 0);
-  for (int kt = 0; kt < KT; ++kt) {
-    wait_vmem();
-    __syncthreads();
-    if (kt + 1 < KT) issue_stage(kt + 1, (kt + 1) & 1);
-    const uint8_t* base = lds + (kt & 1) * STAGE;
+  // Buffer reuse: the copy issued after the barrier of stage kt's last step
+  // goes to buffer (kt-1) % STAGES, whose fragments every wave consumed (its
+  // MFMAs issued) before reaching that barrier; STAGES >= 3 keeps it apart
+  // from buffer (kt+1) % STAGES, read right after.
+  for (int u = 0; u < U; u += 2) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      i32x8 a[TM], b[TN];
+    for (int h = 0; h < 2; ++h) {
+      const int v = u + h;
+      if (v < U) {
+        const int kt = v / SUB, s = v % SUB;
+        int nkt = kt, ns = s + 1;
+        if (ns == SUB) {
+          ns = 0;
+          nkt = kt + 1;
+          if (nkt < KT) {
+            wait_stage_after(kt);
+            if (kt + STAGES - 1 < KT) issue_stage(kt + STAGES - 1);
+          }
+        }
+        // The last step re-reads its own fragments, so the reads are issued on
+        // every path and the MFMAs below wait only for the previous step's.
+        if (nkt >= KT) {
+          nkt = kt;
+          ns = s;
+        }
+        load_frags(nkt, ns, fa[1 - h], fb[1 - h]);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm * WM + i * 32 + frow;
-        const int c0 = (4 * s + fhalf) ^ (r & 7), c1 = (4 * s + fhalf + 1) ^ (r & 7);
-        a[i] = cat8(lds_read16(base + r * kBK + c0 * 16), lds_read16(base + r * kBK + c1 * 16));
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int i = 0; i < TM; ++i) acc[j][i] = mfma_32x32x64_fp8(fa[h][j], fb[h][i], acc[j][i]);
       }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int r = BM + wn * WN + j * 32 + frow;
-        const int c0 = (4 * s + fhalf) ^ (r & 7), c1 = (4 * s + fhalf + 1) ^ (r & 7);
-        b[j] = cat8(lds_read16(base + r * kBK + c0 * 16), lds_read16(base + r * kBK + c1 * 16));
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_32x32x64_fp8(a[i], b[j], acc[i][j]);
     }
   }
 
-  // Epilogue. 32x32 MFMA output layout: lane l holds column l % 32 and, in
-  // register r, row 8*(r/4) + 4*(l/32) + r%4. Rows are tokens, columns channels.
+  // Epilogue. 32x32 MFMA output layout: lane l holds column l % 32 (a token)
+  // and, in register r, row 8*(r/4) + 4*(l/32) + r%4 (a channel): each register
+  // quad is 4 consecutive channels of one token. The finished bf16 tile goes
+  // through LDS ([BM tokens][BN channels], 16-byte chunk c of row r stored at
+  // chunk c ^ (r % OUT_CH)) so that global stores are 16 bytes per lane over
+  // whole row segments.
+  float sxm[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) sxm[i] = scale_lds[wm * WM + i * 32 + (lane & 31)];
+  // Every wave's operand reads are complete before the tile overwrites them.
+  __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+  barrier_only();
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int n = n0 + wn * WN + j * 32 + (lane & 31);
-    if (n >= N) continue;
-    const float swn = ep.sw[n];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int q = 0; q < 4; ++q) {
+      const int nl = wn * WN + j * 32 + 8 * q + 4 * (lane >> 5);  // channel within the tile
+      const int n = n0 + nl;
+      const float4 swq = *reinterpret_cast<const float4*>(scale_lds + BM + nl);
+      const float sw4[4] = {swq.x, swq.y, swq.z, swq.w};
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < M) ep.y[(int64_t)m * ep.ldy + n] = (uint16_t)f32_to_bf16(epilogue_value<RANK>(ep, acc[i][j][r], m, n, ep.sx[m], swn));
+      for (int i = 0; i < TM; ++i) {
+        const int ml = wm * WM + i * 32 + (lane & 31);  // token within the tile
+        const int m = min(m0 + ml, M - 1);
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          h[e] = f32_to_bf16(epilogue_value<RANK>(ep, acc[j][i][4 * q + e], m, min(n + e, N - 1), sxm[i], sw4[e]));
+        const int chunk = (nl >> 3) ^ (ml % OUT_CH);
+        *reinterpret_cast<uint2*>(lds + ml * (BN * 2) + chunk * 16 + (nl & 4) * 2) =
+            uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
       }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+  barrier_only();
+  const bool y_vec = ((ep.ldy | N) & 7) == 0 && (reinterpret_cast<uintptr_t>(ep.y) & 15) == 0;
+  constexpr int NT = 64 * NW;
+#pragma unroll 4
+  for (int c = threadIdx.x; c < BM * OUT_CH; c += NT) {
+    const int ml = c / OUT_CH, ch = c % OUT_CH;
+    const int m = m0 + ml, n = n0 + ch * 8;
+    if (m >= M || n >= N) continue;
+    const uint4 v = *reinterpret_cast<const uint4*>(lds + ml * (BN * 2) + (ch ^ (ml % OUT_CH)) * 16);
+    uint16_t* dst = ep.y + (int64_t)m * ep.ldy + n;
+    if (y_vec) {
+      *reinterpret_cast<uint4*>(dst) = v;
+    } else {
+      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (n + e < N) dst[e] = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
     }
   }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int WGM, int WGN, int BK, int STAGES>
 static hipError_t launch_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
-                                 const Epilogue& ep, int rank, hipStream_t stream) {
+                                 const Epilogue& ep, int rank, int group_m, hipStream_t stream) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-  const dim3 grid((unsigned)(tm * tn)), block(256);
+  const dim3 grid((unsigned)(tm * tn)), block(64 * WGM * WGN);
+  if (group_m < 1) group_m = 1;
   if (rank == 16)
-    gemm_prefill_kernel<BM, BN, 16><<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, ep);
+    gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, 16>
+        <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep);
   else
-    gemm_prefill_kernel<BM, BN, 0><<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, ep);
+    gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, 0>
+        <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep);
   return hipGetLastError();
 }
 
 PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count) {
-  // Largest tile that still gives every CU a workgroup; fall back to smaller ones.
+  // 256x256 tiles (least L2 -> LDS traffic per flop) when they give every CU
+  // at least two; else 256x128 when those give every CU one; else 128x128.
+  // Measured on MI355X over the 9B projection shapes at M = 512..8192.
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-  if (t256 >= cu_count) return PrefillTile{256, 256};
+  if (t256 >= 2 * (int64_t)cu_count) return PrefillTile{256, 256, 2, 4, 64, 4, 4};
   const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
-  if (t256x128 >= cu_count) return PrefillTile{256, 128};
-  return PrefillTile{128, 128};
+  if (t256x128 >= cu_count) return PrefillTile{256, 128, 2, 4, 128, 3, 4};
+  return PrefillTile{128, 128, 2, 2, 128, 4, 8};
 }
 
 hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
-                        const Epilogue& ep, int rank, PrefillTile tile, hipStream_t stream) {
+                        const Epilogue& ep, int rank, PrefillTile t, hipStream_t stream) {
   if (rank != 0 && rank != 16) return hipErrorInvalidValue;
-  if (tile.bm == 256 && tile.bn == 256) return launch_prefill<256, 256>(xq, ldx, w, ldw, M, N, K, ep, rank, stream);
-  if (tile.bm == 256 && tile.bn == 128) return launch_prefill<256, 128>(xq, ldx, w, ldw, M, N, K, ep, rank, stream);
-  if (tile.bm == 128 && tile.bn == 128) return launch_prefill<128, 128>(xq, ldx, w, ldw, M, N, K, ep, rank, stream);
+  if (K % t.bk) return hipErrorInvalidValue;
+#define JV_PREFILL_CASE(BM_, BN_, WGM_, WGN_, BK_, ST_)                                                     \
+  if (t.bm == BM_ && t.bn == BN_ && t.wgm == WGM_ && t.wgn == WGN_ && t.bk == BK_ && t.stages == ST_)       \
+    return launch_prefill<BM_, BN_, WGM_, WGN_, BK_, ST_>(xq, ldx, w, ldw, M, N, K, ep, rank, t.group_m, stream);
+  JV_PREFILL_CASE(256, 256, 4, 2, 64, 3)
+  JV_PREFILL_CASE(256, 256, 4, 2, 64, 4)
+  JV_PREFILL_CASE(256, 256, 2, 4, 64, 3)
+  JV_PREFILL_CASE(256, 256, 2, 4, 64, 4)
+  JV_PREFILL_CASE(256, 128, 2, 4, 128, 3)
+  JV_PREFILL_CASE(256, 128, 4, 2, 128, 3)
+  JV_PREFILL_CASE(256, 128, 2, 4, 64, 4)
+  JV_PREFILL_CASE(256, 128, 4, 2, 64, 4)
+  JV_PREFILL_CASE(128, 256, 2, 4, 128, 3)
+  JV_PREFILL_CASE(128, 256, 2, 4, 64, 4)
+  JV_PREFILL_CASE(128, 128, 2, 2, 128, 3)
+  JV_PREFILL_CASE(128, 128, 2, 2, 128, 4)
+  JV_PREFILL_CASE(128, 128, 2, 2, 64, 4)
+#undef JV_PREFILL_CASE
   return hipErrorInvalidValue;
 }
 

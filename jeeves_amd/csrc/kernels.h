@@ -18,8 +18,11 @@ struct DecodePlan {
   int splits;  // workgroups along K
 };
 
+// Prefill launch shape: output tile bm (tokens) x bn (channels), a wgm x wgn
+// grid of waves per workgroup, K stages of bk bytes in a ring of `stages` LDS
+// buffers, and group_m M-tiles walking N together.
 struct PrefillTile {
-  int bm, bn;
+  int bm, bn, wgm, wgn, bk, stages, group_m;
 };
 
 // Byte offset of activation code (m, k) in the packed decode layout: for
