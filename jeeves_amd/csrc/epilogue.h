@@ -23,10 +23,12 @@ struct Epilogue {
   int64_t ldy;
 };
 
+// biasn: the bias of channel n, already loaded (used only when ep.bias is set).
 template <int RANK>
-__device__ __forceinline__ float epilogue_value(const Epilogue& ep, float acc, int m, int n, float sxm, float swn) {
+__device__ __forceinline__ float epilogue_value(const Epilogue& ep, float acc, int m, int n, float sxm, float swn,
+                                                float biasn) {
   float v = (acc * sxm) * swn;
-  if (ep.bias) v += bf16_to_f32(ep.bias[n]);
+  if (ep.bias) v += biasn;
   if constexpr (RANK > 0) {
     const float* t = ep.lora_t + (int64_t)m * RANK;
     const uint16_t* b = ep.lora_b + (int64_t)n * RANK;
@@ -38,4 +40,9 @@ __device__ __forceinline__ float epilogue_value(const Epilogue& ep, float acc, i
   return v;
 }
 
+// Same with the bias read here.
+template <int RANK>
+__device__ __forceinline__ float epilogue_value(const Epilogue& ep, float acc, int m, int n, float sxm, float swn) {
+  return epilogue_value<RANK>(ep, acc, m, n, sxm, swn, ep.bias ? bf16_to_f32(ep.bias[n]) : 0.0f);
+}
 }  // namespace jv

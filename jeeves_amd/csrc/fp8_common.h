@@ -95,6 +95,53 @@ __device__ __forceinline__ float scale_from_amax_f32(float amax) {
   return fmaxf(amax, kScaleClampMin) * kFp8MaxReciprocal;
 }
 
+// Quantize 8 bf16 (one uint4) with a row's scale (r = RN(1/scale)) to 8 codes
+// (one uint2). fast: the row's maximum is finite, so the scale is finite and
+// positive and the Markstein quotient + hardware converter apply; otherwise
+// the exact division and the spec encoder (inf rows -> zeros, NaN).
+__device__ __forceinline__ uint2 encode8(uint4 v, float scale, float r, bool fast) {
+  float f[8];
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[2 * j] = bf16_to_f32(w[j] & 0xFFFFu);
+    f[2 * j + 1] = bf16_to_f32(w[j] >> 16);
+  }
+  float q[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) q[j] = fast ? __builtin_copysignf(quotient(f[j], scale, r), f[j]) : f[j] / scale;
+  uint2 out;
+  if (fast) {
+    int lo = cvt_pk_fp8<false>(q[0], q[1], 0);
+    lo = cvt_pk_fp8<true>(q[2], q[3], lo);
+    int hi = cvt_pk_fp8<false>(q[4], q[5], 0);
+    hi = cvt_pk_fp8<true>(q[6], q[7], hi);
+    out.x = (uint32_t)lo;
+    out.y = (uint32_t)hi;
+  } else {
+    // inf / NaN rows: exact division and the spec encoder (NaN on overflow).
+    out.x = e4m3_encode_sw(q[0]) | (e4m3_encode_sw(q[1]) << 8) | (e4m3_encode_sw(q[2]) << 16) |
+            (e4m3_encode_sw(q[3]) << 24);
+    out.y = e4m3_encode_sw(q[4]) | (e4m3_encode_sw(q[5]) << 8) | (e4m3_encode_sw(q[6]) << 16) |
+            (e4m3_encode_sw(q[7]) << 24);
+  }
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// Workgroup barriers without the memory fence __syncthreads() carries: that
+// fence makes the compiler drain every outstanding global load first, which
+// empties a kernel's load pipeline. Callers order their own memory.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
+
+// Barrier ordering LDS only: this wave's LDS reads and writes complete
+// (lgkmcnt(0); vmcnt and expcnt left unconstrained), then the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  barrier_no_fence();
+}
+
 // ---------------------------------------------------------------------------
 // Wave64 reductions.
 // ---------------------------------------------------------------------------

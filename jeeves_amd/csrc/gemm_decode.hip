@@ -8,7 +8,10 @@
 //   * each lane streams 32 bytes of one weight row per 128-k step straight
 //     from HBM into MFMA operand registers (no LDS round trip), UNROLL steps
 //     in flight per wave; a wave owns RT 16-row tiles so each activation
-//     fragment it loads feeds RT MFMAs;
+//     fragment it loads feeds RT MFMAs. Plain (cached) loads: on MI355X they
+//     stream these matrices 5-10 % faster than non-temporal ones, and a whole
+//     wave's k range in one burst beats a deeper rolling pipeline (measured
+//     over the 9B projection shapes at M = 1..16);
 //   * activation codes come either row-major [M,K] or, from the fused
 //     quantizer, pre-packed in MFMA B-fragment order (packed_x_offset), so a
 //     wave's activation load is one contiguous 1 KB per instruction;
@@ -67,8 +70,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
       const int64_t off = (int64_t)(s + u) * 128;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        wa[u][rt][0] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wp[rt] + off));
-        wa[u][rt][1] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wp[rt] + off + 16));
+        wa[u][rt][0] = *reinterpret_cast<const i32x4*>(wp[rt] + off);
+        wa[u][rt][1] = *reinterpret_cast<const i32x4*>(wp[rt] + off + 16);
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -139,10 +142,20 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   if (threadIdx.x == 0) __hip_atomic_store(counters + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// k steps per burst for MT token tiles, RT weight tiles and W waves: bounded so
+// the burst's operands fit the registers without spilling.
+constexpr int decode_unroll(int mt, int rt, int w) { return rt + mt > 4 ? 2 : ((w == 8 || rt + mt > 3) ? 4 : 8); }
+
 DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count) {
   DecodePlan p;
   const int64_t tiles = (N + 15) / 16;
+  const int64_t mt = (M + 15) / 16;
   p.rt = tiles >= 4 * (int64_t)cu_count ? 2 : 1;
+  // Four waves take 8 k steps each in one burst up to K = 4096; longer rows
+  // use eight waves in bursts of 4. More token tiles shorten the burst to
+  // bound the registers it holds.
+  p.waves = K / 128 > 32 ? 8 : 4;
+  p.unroll = decode_unroll((int)mt, p.rt, p.waves);
   const int64_t groups = (tiles + p.rt - 1) / p.rt;
   p.groups = (int)groups;
   // Splitting K across workgroups only pays when the tiles cannot occupy an
@@ -150,30 +163,39 @@ DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count) {
   p.splits = 1;
   if (groups * 8 < cu_count) {
     int64_t s = (cu_count + groups - 1) / groups;
-    const int64_t max_s = (K / 128) / kDecodeWaves;
+    const int64_t max_s = (K / 128) / p.waves;
     if (s > max_s) s = max_s;
     if (s > 16) s = 16;
     p.splits = s < 1 ? 1 : (int)s;
   }
-  (void)M;
   return p;
 }
 
-template <int MT, int RT, int U, bool PACKX, int RANK>
+template <int MT, int RT, int W, int U, bool PACKX, int RANK>
 static void launch_decode(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
                           const DecodePlan& p, float* partial, int* counters, const Epilogue& ep, hipStream_t stream) {
-  const dim3 grid((unsigned)p.groups, (unsigned)p.splits), block(64 * kDecodeWaves);
-  gemm_decode_kernel<MT, RT, kDecodeWaves, U, PACKX, RANK>
+  const dim3 grid((unsigned)p.groups, (unsigned)p.splits), block(64 * W);
+  gemm_decode_kernel<MT, RT, W, U, PACKX, RANK>
       <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, p.splits, partial, counters, ep);
+}
+
+template <int MT, int RT, bool PACKX, int RANK>
+static void launch_decode_wu(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                             const DecodePlan& p, float* partial, int* counters, const Epilogue& ep, hipStream_t stream) {
+  constexpr int U4 = decode_unroll(MT, RT, 4), U8 = decode_unroll(MT, RT, 8);
+  if (p.waves == 8)
+    launch_decode<MT, RT, 8, U8, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+  else
+    launch_decode<MT, RT, 4, U4, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
 }
 
 template <int MT, bool PACKX, int RANK>
 static void launch_decode_rt(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
                              const DecodePlan& p, float* partial, int* counters, const Epilogue& ep, hipStream_t stream) {
   if (p.rt == 2)
-    launch_decode<MT, 2, 4, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+    launch_decode_wu<MT, 2, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
   else
-    launch_decode<MT, 1, 8, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+    launch_decode_wu<MT, 1, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
 }
 
 template <bool PACKX, int RANK>

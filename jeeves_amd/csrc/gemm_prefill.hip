@@ -36,12 +36,10 @@ __device__ __forceinline__ void wait_vmem_below() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Workgroup barrier without the memory fence __syncthreads() carries (the
-// fence makes the compiler drain every outstanding load first, which would
-// empty the copy pipeline). Callers order their own memory: each wave waits
-// for its global -> LDS copies with wait_vmem_below before the barrier, and
-// has consumed its earlier LDS reads (their MFMAs issued) before reaching it.
-__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+// Main-loop barrier: each wave waits for its global -> LDS copies with
+// wait_vmem_below before it, and has consumed its earlier LDS reads (their
+// MFMAs issued) before reaching it.
+__device__ __forceinline__ void barrier_only() { barrier_no_fence(); }
 
 // Copy 16 bytes per lane from global to LDS: lane i's bytes land at dst + 16 * i.
 __device__ __forceinline__ void load_lds16(const uint8_t* src, uint8_t* dst_wave_base) {
@@ -246,8 +244,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
 #pragma unroll
   for (int i = 0; i < TM; ++i) sxm[i] = scale_lds[wm * WM + i * 32 + (lane & 31)];
   // Every wave's operand reads are complete before the tile overwrites them.
-  __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
-  barrier_only();
+  lds_barrier();
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -270,8 +267,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
       }
     }
   }
-  __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
-  barrier_only();
+  lds_barrier();
   const bool y_vec = ((ep.ldy | N) & 7) == 0 && (reinterpret_cast<uintptr_t>(ep.y) & 15) == 0;
   constexpr int NT = 64 * NW;
 #pragma unroll 4

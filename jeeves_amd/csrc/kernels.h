@@ -10,10 +10,11 @@ namespace jv {
 
 // Decode regime: M <= kDecodeMaxRows tokens.
 constexpr int kDecodeMaxRows = 64;
-constexpr int kDecodeWaves = 4;
 
 struct DecodePlan {
   int rt;      // 16-row tiles per wave
+  int waves;   // waves per workgroup, splitting the workgroup's k range
+  int unroll;  // k steps of 128 loaded per burst
   int groups;  // workgroups along N
   int splits;  // workgroups along K
 };

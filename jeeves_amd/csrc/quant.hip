@@ -35,36 +35,6 @@ __device__ __forceinline__ uint32_t swiglu_pair(uint32_t g2, uint32_t u2) {
   return swiglu_bf16(g2 & 0xFFFFu, u2 & 0xFFFFu) | (swiglu_bf16(g2 >> 16, u2 >> 16) << 16);
 }
 
-// Encode 8 bf16 (one uint4) to 8 codes (one uint2).
-__device__ __forceinline__ uint2 encode8(uint4 v, float scale, float r, bool fast) {
-  float f[8];
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    f[2 * j] = bf16_to_f32(w[j] & 0xFFFFu);
-    f[2 * j + 1] = bf16_to_f32(w[j] >> 16);
-  }
-  float q[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) q[j] = fast ? __builtin_copysignf(quotient(f[j], scale, r), f[j]) : f[j] / scale;
-  uint2 out;
-  if (fast) {
-    int lo = cvt_pk_fp8<false>(q[0], q[1], 0);
-    lo = cvt_pk_fp8<true>(q[2], q[3], lo);
-    int hi = cvt_pk_fp8<false>(q[4], q[5], 0);
-    hi = cvt_pk_fp8<true>(q[6], q[7], hi);
-    out.x = (uint32_t)lo;
-    out.y = (uint32_t)hi;
-  } else {
-    // inf / NaN rows: exact division and the spec encoder (NaN on overflow).
-    out.x = e4m3_encode_sw(q[0]) | (e4m3_encode_sw(q[1]) << 8) | (e4m3_encode_sw(q[2]) << 16) |
-            (e4m3_encode_sw(q[3]) << 24);
-    out.y = e4m3_encode_sw(q[4]) | (e4m3_encode_sw(q[5]) << 8) | (e4m3_encode_sw(q[6]) << 16) |
-            (e4m3_encode_sw(q[7]) << 24);
-  }
-  return out;
-}
-
 template <int RANK>
 __device__ __forceinline__ void lora_accumulate(float (&t)[RANK > 0 ? RANK : 1], uint4 v, const uint16_t* __restrict__ a,
                                                 int64_t K, int c) {

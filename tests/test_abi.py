@@ -76,7 +76,7 @@ def test_split_for_is_pure_host_logic(product_lib):
     assert L.jv_fp8_split_for(16, 1024, 4096, 256) == 1
     assert L.jv_fp8_split_for(16, 24576, 4096, 256) == 1
     assert L.jv_fp8_split_for(16, 256, 4096, 256) == 8   # 16 tiles, capped at K/128/4
-    assert L.jv_fp8_split_for(16, 128, 12288, 256) == 16  # 8 tiles, capped at 16
+    assert L.jv_fp8_split_for(16, 128, 12288, 256) == 12  # 8 tiles; K=12288 runs 8 waves: capped at K/128/8
     assert L.jv_fp8_split_for(2048, 128, 4096, 256) == 1  # prefill never splits
     assert L.jv_fp8_counters_needed(16, 256, 4096, 256) == 16
     assert L.jv_fp8_counters_needed(16, 4096, 4096, 256) == 0

@@ -75,17 +75,29 @@ def test_reference_acceptance_cases(weights, N, K, M):
 @pytest.mark.parametrize("name", list(synthetic.SHAPES))
 @pytest.mark.parametrize("M", synthetic.DECODE_ROWS + (64,))
 def test_decode_workload_shapes(name, M):
+    """Both decode entry points: fp8_matmul (activation codes packed in MFMA
+    fragment order by the quantizer) and the GEMM on row-major codes. Without
+    split-K both sum every output in the same order, so they agree bitwise."""
     x, w = synthetic.decode_case(name, M)
     wq, sw = quantize_rows(w.cuda())
     x = x.cuda()
-    check(fp8_matmul(x, wq, sw), x, wq, sw)
+    y = fp8_matmul(x, wq, sw)
+    check(y, x, wq, sw)
+    xq, sx = quantize_rows(x)
+    yq = fp8_matmul_quantized(xq, sx, wq, sw)
+    check(yq, x, wq, sw)
+    N, K = wq.shape
+    if _lib.lib().jv_fp8_split_for(M, N, K, torch.cuda.get_device_properties(0).multi_processor_count) == 1:
+        assert torch.equal(y, yq)
 
 
-@pytest.mark.parametrize("N,K", [(256, 4096), (128, 12288), (144, 1024)])
+@pytest.mark.parametrize("N,K", [(256, 4096), (128, 12288), (144, 1024), (144, 2048)])
 @pytest.mark.parametrize("M", [1, 16, 33, 64])
 def test_split_k_decode_path(N, K, M):
     """Narrow weights (N < 512) split K across workgroups; the last workgroup of
-    each tile sums the partials in split order and leaves the counters zero."""
+    each tile sums the partials in split order and leaves the counters zero.
+    Both entry points (fp8_matmul on bf16 activations, and the GEMM on
+    activations already quantized) take the split path."""
     from jeeves_amd import TILE_COUNTERS
     from jeeves_amd.device import sm_count
 
@@ -94,11 +106,28 @@ def test_split_k_decode_path(N, K, M):
     w = synthetic.weight(N, K, 71)
     wq, sw = quantize_rows(w.cuda())
     x = x.cuda()
-    y = fp8_matmul(x, wq, sw)
+    xq, sx = quantize_rows(x)
+    y = fp8_matmul_quantized(xq, sx, wq, sw)
     check(y, x, wq, sw)
-    assert torch.equal(y, fp8_matmul(x, wq, sw)), "split-K result is not deterministic"
+    assert torch.equal(y, fp8_matmul_quantized(xq, sx, wq, sw)), "split-K result is not deterministic"
+    y2 = fp8_matmul(x, wq, sw)
+    check(y2, x, wq, sw)
+    assert torch.equal(y2, fp8_matmul(x, wq, sw))
     torch.cuda.synchronize()
     assert all(int(c.abs().sum()) == 0 for c in TILE_COUNTERS.values())
+
+
+@pytest.mark.parametrize("N,K", [(144, 1024), (160, 384), (48, 128), (4112, 256)])
+@pytest.mark.parametrize("M", [1, 5, 16, 40])
+def test_decode_short_k(N, K, M):
+    """K below 4 steps of 128 per wave (some waves of the decode workgroup get
+    no k step), odd tile counts, both decode entry points."""
+    x = synthetic.activations_heavy_tail(M, K, 90 + M)
+    wq, sw = quantize_rows(synthetic.weight(N, K, 91).cuda())
+    x = x.cuda()
+    check(fp8_matmul(x, wq, sw), x, wq, sw)
+    xq, sx = quantize_rows(x)
+    check(fp8_matmul_quantized(xq, sx, wq, sw), x, wq, sw)
 
 
 @pytest.mark.parametrize("name", list(synthetic.SHAPES))
