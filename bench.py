@@ -101,15 +101,35 @@ def build_set(torch, synthetic, quantize_rows, M: int, case):
     return rot, xs, copies, per_copy
 
 
-def kernel_ms(b: Bench, fp8, rot, xq, sx, name: str, replays: int) -> float:
-    """Average time (ms) of one GEMM kernel launch for projection `name` on
-    pre-quantized activations, from graphs of back-to-back launches."""
+def quantized_operands(torch, fp8, x):
+    """Activation codes as fp8_matmul hands them to its GEMM: packed fragment
+    order for decode batches, row-major above."""
+    from jeeves_amd import _lib
+
+    M, K = x.shape
+    sx = torch.empty(M, dtype=torch.float32, device=x.device)
+    if M <= fp8.DECODE_MAX_ROWS:
+        codes = torch.empty(fp8.packed_codes_bytes(M, K), dtype=torch.uint8, device=x.device)
+        _lib.check(_lib.lib().jv_fp8_quantize_rows_bf16(x.data_ptr(), x.stride(0), M, K, codes.data_ptr(), 0, sx.data_ptr(),
+                                                        torch.cuda.current_stream().cuda_stream))
+        return codes, sx, M
+    codes = torch.empty(M, K, dtype=torch.uint8, device=x.device)
+    _lib.check(_lib.lib().jv_fp8_quantize_rows_bf16(x.data_ptr(), x.stride(0), M, K, codes.data_ptr(), K, sx.data_ptr(),
+                                                    torch.cuda.current_stream().cuda_stream))
+    return codes, sx, None
+
+
+def kernel_ms(b: Bench, fp8, rot, operands, name: str, replays: int) -> float:
+    """Average time (ms) of one GEMM kernel launch for projection `name` on the
+    activation codes fp8_matmul would produce, from graphs of back-to-back
+    launches on the bench stream."""
+    xq, sx, packed_rows = operands
     graphs = []
     for c in range(len(rot)):
         def launches(c=c):
             for j in range(LAUNCHES_PER_GRAPH):
                 wq, sw = rot[(c + j) % len(rot)][name]
-                fp8.fp8_matmul_quantized(xq, sx, wq, sw)
+                fp8.fp8_matmul_quantized(xq, sx, wq, sw, packed_rows=packed_rows)
         graphs.append(b.capture(launches))
     return b.time_graphs(graphs, replays, 3) / LAUNCHES_PER_GRAPH
 
@@ -185,8 +205,7 @@ def main() -> int:
 
     per_shape = {}
     for name, (n_, k_) in synthetic.SHAPES.items():
-        q_, s_ = quantize_rows(xs[name])
-        t = kernel_ms(b, fp8, rot, q_, s_, name, 40)
+        t = kernel_ms(b, fp8, rot, quantized_operands(torch, fp8, xs[name]), name, 40)
         per_shape[name] = {"us": round(t * 1e3, 2), "GB/s": round(linear_bytes(M, n_, k_) / (t * 1e-3) / 1e9, 1)}
     N, K = synthetic.SHAPES["gate_up"]
     k_ms = per_shape["gate_up"]["us"] * 1e-3
@@ -237,8 +256,7 @@ def main() -> int:
         pms = b.time_graphs(pgraphs, max(args.steps // 8, 20), 3)
         pshape = {}
         for name, (n_, k_) in synthetic.SHAPES.items():
-            q_, s_ = quantize_rows(pxs[name])
-            t = kernel_ms(b, fp8, prot, q_, s_, name, 8)
+            t = kernel_ms(b, fp8, prot, quantized_operands(torch, fp8, pxs[name]), name, 8)
             pshape[name] = {"us": round(t * 1e3, 2), "TFLOP/s": round(2 * Mp * n_ * k_ / (t * 1e-3) / 1e12, 1)}
         pk = pshape["gate_up"]["us"] * 1e-3
         pk_tf = 2 * Mp * N * K / (pk * 1e-3) / 1e12

@@ -53,10 +53,20 @@ int jv_device_cu_count(int device);
  *   codes[r,c] = e4m3fn(x[r,c] / scales[r])   (IEEE quotient, RNE, NaN on overflow)
  * x: [rows, cols] bf16, row stride ldx; codes: [rows, cols] bytes, row stride
  * ldc; scales: [rows] fp32. cols must be a positive multiple of 8.
+ * ldc = 0 writes the codes in the decode GEMM's packed fragment order instead
+ * (rows <= JV_FP8_DECODE_MAX_ROWS, cols a multiple of 128 up to 16384; the
+ * buffer holds jv_fp8_packed_codes_bytes(rows, cols) bytes), for jv_fp8_gemm
+ * with ldxq = 0.
  * Used for per-token activation quantization and for FP8Linear.load_weight
  * (inference/fp8.py:164-166). */
 int jv_fp8_quantize_rows_bf16(const void* x, int64_t ldx, int64_t rows, int64_t cols, void* codes, int64_t ldc,
                               float* scales, void* stream);
+
+/* Bytes of rows x cols activation codes in the packed fragment order (rows
+ * padded to a multiple of 16), or -1 when the layout does not apply. The
+ * counterpart of the fp16 row copies fp8_matmul allocates
+ * (inference/fp8.py:142-143). */
+int64_t jv_fp8_packed_codes_bytes(int64_t rows, int64_t cols);
 
 /* Same for float32 rows (FP8Linear.load_weight given fp32 weights). cols must be a
  * positive multiple of 4. */
@@ -94,8 +104,10 @@ int64_t jv_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* The GEMM and epilogue alone on already-quantized activations
  * (_fp8_matmul, inference/fp8.py:62-99, with FP8 x FP8 operands):
- * xq: [M,K] e4m3fn (row stride ldxq); x_scale: [M] fp32; lora_t: [M,rank]
- * fp32 low-rank activations or NULL; other arguments as jv_fp8_linear. */
+ * xq: [M,K] e4m3fn (row stride ldxq; ldxq = 0: the packed fragment order of
+ * jv_fp8_quantize_rows_bf16 with ldc = 0, M <= JV_FP8_DECODE_MAX_ROWS);
+ * x_scale: [M] fp32; lora_t: [M,rank] fp32 low-rank activations or NULL;
+ * other arguments as jv_fp8_linear. */
 int jv_fp8_gemm(const void* xq, int64_t ldxq, const float* x_scale, const void* w, int64_t ldw, const float* w_scale,
                 const void* bias, const float* lora_t, const void* lora_b, int64_t lora_rank, float lora_scaling, void* y,
                 int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
@@ -105,7 +117,8 @@ int jv_fp8_gemm(const void* xq, int64_t ldxq, const float* x_scale, const void* 
  * model/model.py:581-584) fused with the down projection's per-token
  * quantization: h = bf16(bf16(silu(gate)) * up), then quantize_rows(h).
  * gate, up: [M,I] bf16 (may be the two halves of one fused gate+up output);
- * codes: [M,I]; scales: [M]; h_out: [M,I] bf16 copy of h or NULL; lora_a:
+ * codes: [M,I] with row stride ldc (ldc = 0: packed fragment order, as for
+ * jv_fp8_quantize_rows_bf16); scales: [M]; h_out: [M,I] bf16 copy of h or NULL; lora_a:
  * [rank,I] bf16 with lora_t: [M,rank] fp32 output (h A^T), or NULL/0.
  * I must be a positive multiple of 8 and at most 16384. */
 int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_t ldu, int64_t M, int64_t I, void* codes,

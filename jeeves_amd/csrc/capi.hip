@@ -117,11 +117,20 @@ int jv_fp8_quantize_rows_bf16(const void* x, int64_t ldx, int64_t rows, int64_t 
   if (rows < 0 || cols <= 0 || cols % 8 || cols > INT32_MAX || rows > INT32_MAX)
     return fail(JV_ERR_VALUE, "quantize_rows needs a positive column count divisible by 8, got %lld", (long long)cols);
   if (rows == 0) return JV_OK;
+  const bool packed = ldc == 0;
+  if (packed && (rows > jv::kDecodeMaxRows || cols % JV_FP8_BLOCK_K || jv::quant_chunks((int)cols) == 0))
+    return fail(JV_ERR_VALUE, "the packed layout needs at most %d rows and a column count divisible by %d up to 16384",
+                jv::kDecodeMaxRows, JV_FP8_BLOCK_K);
   if (!aligned16(x) || (ldx * 2) % 16 || !aligned16(codes) || ldc % 16)
     return fail(JV_ERR_VALUE, "quantize_rows needs 16-byte aligned rows");
   return hip_status(jv::quant_rows_bf16((const uint16_t*)x, ldx, rows, (int)cols, (uint8_t*)codes, ldc, scales, nullptr, 0,
-                                        nullptr, false, (hipStream_t)stream),
+                                        nullptr, packed, (hipStream_t)stream),
                     "quantize_rows launch");
+}
+
+int64_t jv_fp8_packed_codes_bytes(int64_t rows, int64_t cols) {
+  if (rows < 0 || rows > jv::kDecodeMaxRows || cols <= 0 || cols % JV_FP8_BLOCK_K) return -1;
+  return jv::packed_x_bytes(rows, cols);
 }
 
 int jv_fp8_quantize_rows_f32(const float* x, int64_t ldx, int64_t rows, int64_t cols, void* codes, int64_t ldc,
@@ -154,9 +163,12 @@ int jv_fp8_gemm(const void* xq, int64_t ldxq, const float* x_scale, const void* 
   if (int rc = check_gemm_shape(M, N, K)) return rc;
   if (int rc = check_lora(lora_rank, lora_t, lora_b)) return rc;
   if (M == 0) return JV_OK;
+  const bool packed = ldxq == 0;
+  if (packed && M > jv::kDecodeMaxRows)
+    return fail(JV_ERR_VALUE, "packed activation codes hold at most %d rows, got %lld", jv::kDecodeMaxRows, (long long)M);
   if (!aligned16(xq) || ldxq % 16 || !aligned16(w) || ldw % 16)
     return fail(JV_ERR_VALUE, "the fp8 GEMM needs 16-byte aligned operand rows");
-  return run_gemm((const uint8_t*)xq, ldxq, false, x_scale, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t,
+  return run_gemm((const uint8_t*)xq, ldxq, packed, x_scale, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t,
                   (const uint16_t*)lora_b, lora_rank, lora_scaling, (uint16_t*)y, ldy, M, N, K, (uint8_t*)workspace,
                   workspace_bytes, tile_counters, n_counters, (hipStream_t)stream);
 }
@@ -201,12 +213,16 @@ int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_
     return fail(JV_ERR_VALUE, "swiglu_quantize needs 0 < I <= 16384 divisible by 8, got %lld", (long long)I);
   if (int rc = check_lora(lora_rank, lora_a, lora_t)) return rc;
   if (M == 0) return JV_OK;
+  const bool packed = ldc == 0;
+  if (packed && (M > jv::kDecodeMaxRows || I % JV_FP8_BLOCK_K))
+    return fail(JV_ERR_VALUE, "the packed layout needs at most %d rows and I divisible by %d", jv::kDecodeMaxRows,
+                JV_FP8_BLOCK_K);
   if (!aligned16(gate) || (ldg * 2) % 16 || !aligned16(up) || (ldu * 2) % 16 || !aligned16(codes) || ldc % 16 ||
       (h_out && (!aligned16(h_out) || (ldh * 2) % 16)))
     return fail(JV_ERR_VALUE, "swiglu_quantize needs 16-byte aligned rows");
   return hip_status(jv::quant_swiglu_bf16((const uint16_t*)gate, ldg, (const uint16_t*)up, ldu, M, (int)I, (uint8_t*)codes,
                                           ldc, scales, (uint16_t*)h_out, ldh, (const uint16_t*)lora_a, (int)lora_rank,
-                                          lora_t, (hipStream_t)stream),
+                                          lora_t, packed, (hipStream_t)stream),
                     "swiglu_quantize launch");
 }
 

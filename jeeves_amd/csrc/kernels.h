@@ -45,7 +45,7 @@ hipError_t quant_rows_bf16(const uint16_t* x, int64_t ldx, int64_t M, int K, uin
                            const uint16_t* lora_a, int rank, float* lora_t, bool packed, hipStream_t stream);
 hipError_t quant_swiglu_bf16(const uint16_t* gate, int64_t ldg, const uint16_t* up, int64_t ldu, int64_t M, int K,
                              uint8_t* codes, int64_t ldc, float* scales, uint16_t* h_out, int64_t ldh,
-                             const uint16_t* lora_a, int rank, float* lora_t, hipStream_t stream);
+                             const uint16_t* lora_a, int rank, float* lora_t, bool packed, hipStream_t stream);
 hipError_t quant_rows_f32(const float* x, int64_t ldx, int64_t M, int K, uint8_t* codes, int64_t ldc, float* scales,
                           hipStream_t stream);
 

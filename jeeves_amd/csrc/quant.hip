@@ -268,10 +268,18 @@ hipError_t quant_rows_bf16(const uint16_t* x, int64_t ldx, int64_t M, int K, uin
 
 hipError_t quant_swiglu_bf16(const uint16_t* gate, int64_t ldg, const uint16_t* up, int64_t ldu, int64_t M, int K,
                              uint8_t* codes, int64_t ldc, float* scales, uint16_t* h_out, int64_t ldh,
-                             const uint16_t* lora_a, int rank, float* lora_t, hipStream_t stream) {
+                             const uint16_t* lora_a, int rank, float* lora_t, bool packed, hipStream_t stream) {
   if (M == 0) return hipSuccess;
   const int nc = quant_chunks(K);
   if (nc == 0) return hipErrorInvalidValue;
+  if (packed) {
+    if (M > kDecodeMaxRows || (K & 127)) return hipErrorInvalidValue;
+    if (rank == 0)
+      return launch_rows<true, 0, true>(nc, gate, ldg, up, ldu, M, K, codes, 0, scales, h_out, ldh, nullptr, nullptr, stream);
+    if (rank == 16)
+      return launch_rows<true, 16, true>(nc, gate, ldg, up, ldu, M, K, codes, 0, scales, h_out, ldh, lora_a, lora_t, stream);
+    return hipErrorInvalidValue;
+  }
   if (rank == 0)
     return launch_rows<true, 0>(nc, gate, ldg, up, ldu, M, K, codes, ldc, scales, h_out, ldh, nullptr, nullptr, stream);
   if (rank == 16)

@@ -133,21 +133,39 @@ def fp8_matmul(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *, bi
     return y
 
 
+def packed_codes_bytes(rows: int, cols: int) -> int:
+    """Bytes of ``rows x cols`` activation codes in the decode GEMM's packed
+    fragment order (rows <= ``DECODE_MAX_ROWS``, cols a multiple of 128)."""
+    n = _lib.lib().jv_fp8_packed_codes_bytes(rows, cols)
+    if n < 0:
+        raise ValueError(f"the packed layout takes at most {DECODE_MAX_ROWS} rows and a multiple of {BLOCK_K} columns, "
+                         f"got {rows} x {cols}")
+    return n
+
+
 def fp8_matmul_quantized(xq: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *,
                          bias: torch.Tensor | None = None, lora_t: torch.Tensor | None = None,
-                         lora_b: torch.Tensor | None = None, lora_scaling: float = 0.0) -> torch.Tensor:
+                         lora_b: torch.Tensor | None = None, lora_scaling: float = 0.0,
+                         packed_rows: int | None = None) -> torch.Tensor:
     """The GEMM alone on activations already quantized per token (codes
     float8_e4m3fn/uint8 [M,K] and scales float32 [M]), e.g. by
-    ``swiglu_quantize``. ``lora_t`` is ``x A^T`` (float32 [M,r])."""
-    M, K = xq.shape
+    ``swiglu_quantize``. ``lora_t`` is ``x A^T`` (float32 [M,r]).
+    ``packed_rows=M``: ``xq`` is a flat uint8 buffer of M token rows in the
+    packed fragment order (``swiglu_quantize(..., packed=True)``)."""
     N = weight.shape[0]
+    if packed_rows is not None:
+        M, K = packed_rows, weight.shape[1]
+        if xq.dim() != 1 or xq.numel() < packed_codes_bytes(M, K):
+            raise ValueError(f"packed codes for {M} x {K} need {packed_codes_bytes(M, K)} bytes")
+    else:
+        M, K = xq.shape
     _check_weight(K, weight)
     rank = 0 if lora_t is None else lora_t.shape[1]
     if rank and (rank not in LORA_RANKS or lora_b is None or lora_b.shape != (N, rank)):
         raise ValueError("lora_t needs lora_b [N, r] with r in (16,)")
     dev = xq.device
     xq = xq.view(torch.uint8)
-    if not _rows_aligned(xq, 1):
+    if packed_rows is None and not _rows_aligned(xq, 1):
         xq = xq.contiguous()
     w = weight.view(torch.uint8)
     if not _rows_aligned(w, 1):
@@ -166,7 +184,8 @@ def fp8_matmul_quantized(xq: torch.Tensor, x_scale: torch.Tensor, weight: torch.
         if ws_bytes < 0:
             _lib.check(_lib.JV_ERR_HIP)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-        _lib.check(L.jv_fp8_gemm(xq.data_ptr(), xq.stride(0), x_scale.to(torch.float32).contiguous().data_ptr(), w.data_ptr(),
+        _lib.check(L.jv_fp8_gemm(xq.data_ptr(), 0 if packed_rows is not None else xq.stride(0),
+                                 x_scale.to(torch.float32).contiguous().data_ptr(), w.data_ptr(),
                                  w.stride(0), scale.to(torch.float32).contiguous().data_ptr(),
                                  bias.data_ptr() if bias is not None else None, lora_t.data_ptr() if rank else None,
                                  lora_b.data_ptr() if rank else None, rank, float(lora_scaling), y.data_ptr(), N, M, N, K,
@@ -176,11 +195,12 @@ def fp8_matmul_quantized(xq: torch.Tensor, x_scale: torch.Tensor, weight: torch.
 
 
 def swiglu_quantize(gate: torch.Tensor, up: torch.Tensor, *, lora_a: torch.Tensor | None = None,
-                    return_h: bool = False) -> tuple[torch.Tensor, ...]:
+                    return_h: bool = False, packed: bool = False) -> tuple[torch.Tensor, ...]:
     """``h = F.silu(gate) * up`` on bf16 (``model/model.py:583``) fused with the
     down projection's per-token quantization. Returns ``(codes, scales)``, plus
     ``t = h A^T`` (float32 [M,r]) when ``lora_a`` is given and ``h`` (bf16) when
-    ``return_h``."""
+    ``return_h``. ``packed``: codes come as a flat uint8 buffer in the decode
+    GEMM's fragment order, for ``fp8_matmul_quantized(..., packed_rows=M)``."""
     M, I = gate.shape
     if up.shape != gate.shape:
         raise ValueError(f"gate {tuple(gate.shape)} and up {tuple(up.shape)} differ")
@@ -190,7 +210,7 @@ def swiglu_quantize(gate: torch.Tensor, up: torch.Tensor, *, lora_a: torch.Tenso
         gate = gate.contiguous()
     if not _rows_aligned(up, 2):
         up = up.contiguous()
-    codes = torch.empty(M, I, dtype=torch.uint8, device=dev)
+    codes = torch.empty(packed_codes_bytes(M, I) if packed else (M, I), dtype=torch.uint8, device=dev)
     scales = torch.empty(M, dtype=torch.float32, device=dev)
     h = torch.empty(M, I, dtype=torch.bfloat16, device=dev) if return_h else None
     rank = 0
@@ -204,11 +224,11 @@ def swiglu_quantize(gate: torch.Tensor, up: torch.Tensor, *, lora_a: torch.Tenso
     if M:
         with torch.cuda.device(dev):
             _lib.check(_lib.lib().jv_fp8_swiglu_quantize(gate.data_ptr(), gate.stride(0), up.data_ptr(), up.stride(0), M, I,
-                                                         codes.data_ptr(), I, scales.data_ptr(),
+                                                         codes.data_ptr(), 0 if packed else I, scales.data_ptr(),
                                                          h.data_ptr() if h is not None else None, I,
                                                          lora_a.data_ptr() if rank else None, rank,
                                                          t.data_ptr() if rank else None, _stream(dev)))
-    out: tuple[torch.Tensor, ...] = (codes.view(FP8), scales)
+    out: tuple[torch.Tensor, ...] = (codes if packed else codes.view(FP8), scales)
     if rank:
         out += (t,)
     if return_h:
@@ -275,13 +295,17 @@ class FP8SwiGLU(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shape = x.shape
         gu = self.gate_up(x.reshape(-1, shape[-1]))
+        M = gu.shape[0]
         inter = self.down.in_features
         lora_a = self.down.lora[0] if self.down.lora is not None else None
-        out = swiglu_quantize(gu[:, :inter], gu[:, inter:], lora_a=lora_a)
+        # Decode batches hand the down GEMM its codes in fragment order.
+        packed = 0 < M <= DECODE_MAX_ROWS and inter % BLOCK_K == 0
+        out = swiglu_quantize(gu[:, :inter], gu[:, inter:], lora_a=lora_a, packed=packed)
         lora_t = out[2] if lora_a is not None else None
         y = fp8_matmul_quantized(out[0], out[1], self.down.weight, self.down.scale, bias=self.down.bias, lora_t=lora_t,
                                  lora_b=self.down.lora[1] if lora_a is not None else None,
-                                 lora_scaling=self.down.lora[2] if lora_a is not None else 0.0)
+                                 lora_scaling=self.down.lora[2] if lora_a is not None else 0.0,
+                                 packed_rows=M if packed else None)
         return y.view(*shape[:-1], self.down.out_features)
 
 

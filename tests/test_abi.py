@@ -82,6 +82,15 @@ def test_split_for_is_pure_host_logic(product_lib):
     assert L.jv_fp8_counters_needed(16, 4096, 4096, 256) == 0
 
 
+def test_packed_layout_sizes_are_host_logic(product_lib):
+    L = product_lib
+    assert L.jv_fp8_packed_codes_bytes(16, 4096) == 16 * 4096
+    assert L.jv_fp8_packed_codes_bytes(17, 4096) == 32 * 4096   # rows pad to 16
+    assert L.jv_fp8_packed_codes_bytes(1, 128) == 16 * 128
+    assert L.jv_fp8_packed_codes_bytes(65, 4096) == -1          # decode batches only
+    assert L.jv_fp8_packed_codes_bytes(16, 100) == -1           # K must be a multiple of 128
+
+
 def test_hook_library_exports(hooks_lib):
     for name in ("th_encode", "th_encode_sweep", "th_quotient_sweep", "th_mfma32", "th_mfma16"):
         assert hasattr(hooks_lib, name)

@@ -17,7 +17,7 @@ import torch
 
 import oracle
 from jeeves_amd import _lib, synthetic
-from jeeves_amd.fp8 import fp8_matmul, fp8_matmul_quantized
+from jeeves_amd.fp8 import fp8_matmul, fp8_matmul_quantized, swiglu_quantize
 from jeeves_amd.fp8_weights import FP8, quantize_rows
 from tests import helpers
 
@@ -235,3 +235,43 @@ def test_graph_capture_and_replay():
             eager = fp8_matmul(x, wq, sw)
             torch.cuda.synchronize()
             assert torch.equal(static_y, eager), (M, seed)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 33, 64])
+@pytest.mark.parametrize("N,K", [(1024, 4096), (4096, 12288), (256, 384)])
+def test_packed_activation_codes(M, N, K):
+    """Codes written in the decode GEMM's packed fragment order (ldc = 0) and
+    consumed with ldxq = 0 give the same output, bit for bit, as row-major
+    codes; the scales are the row-major quantizer's."""
+    from jeeves_amd.fp8 import packed_codes_bytes
+
+    x = synthetic.activations_heavy_tail(M, K, 120 + M).cuda()
+    wq, sw = quantize_rows(synthetic.weight(N, K, 121).cuda())
+    xq, sx = quantize_rows(x)
+    packed = torch.full((packed_codes_bytes(M, K),), 0xAA, dtype=torch.uint8, device="cuda")
+    psx = torch.full((M,), float("nan"), device="cuda")
+    L = _lib.lib()
+    _lib.check(L.jv_fp8_quantize_rows_bf16(x.data_ptr(), K, M, K, packed.data_ptr(), 0, psx.data_ptr(), helpers.stream()))
+    assert helpers.same_f32(psx.cpu().numpy(), sx.cpu().numpy()).all()
+    y_row = fp8_matmul_quantized(xq, sx, wq, sw)
+    y_packed = fp8_matmul_quantized(packed, psx, wq, sw, packed_rows=M)
+    assert torch.equal(y_row, y_packed)
+    check(y_packed, x, wq, sw)
+    # padding rows of the last 16-token tile hold zero codes
+    assert int(packed.long().sum().item()) == int(xq.view(torch.uint8).long().sum().item())
+
+
+@pytest.mark.parametrize("M", [1, 16, 40])
+def test_swiglu_packed_codes_feed_down_projection(M):
+    I, N = 4096, 1024
+    g = torch.Generator().manual_seed(130 + M)
+    gate = (torch.randn(M, I, generator=g) * 2).to(torch.bfloat16).cuda()
+    up = torch.randn(M, I, generator=g).to(torch.bfloat16).cuda()
+    wq, sw = quantize_rows(synthetic.weight(N, I, 131).cuda())
+    codes, scales, h = swiglu_quantize(gate, up, return_h=True)
+    pcodes, pscales, ph = swiglu_quantize(gate, up, return_h=True, packed=True)
+    assert torch.equal(scales, pscales) and torch.equal(h, ph)
+    y_row = fp8_matmul_quantized(codes, scales, wq, sw)
+    y_packed = fp8_matmul_quantized(pcodes, pscales, wq, sw, packed_rows=M)
+    assert torch.equal(y_row, y_packed)
+    check(y_packed, h, wq, sw)
