@@ -44,6 +44,19 @@ ROTATE_BYTES = 512 << 20
 LAUNCHES_PER_GRAPH = 24
 
 
+def measured_traffic(key: str):
+    """HBM bytes per launch measured with rocprofv3 PMC counters, from the
+    committed summary (None when absent)."""
+    path = ROOT / "profiles" / "gate_up_hbm_traffic_pmc.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == key:
+            return int(parts[2])
+    return None
+
+
 def linear_bytes(M: int, N: int, K: int) -> int:
     return N * K + 4 * N + 2 * M * K + 2 * M * N
 
@@ -162,6 +175,30 @@ def cpu_baseline(synthetic, M: int, budget_s: float) -> dict:
                       f"float32 sgemm, bf16 rounding) in {elapsed:.1f} s"}
 
 
+def pmc_driver(torch, fp8, synthetic, quantize_rows, launches: int = 10) -> None:
+    """Workload for the hardware-counter runs (rocprofv3 --pmc FETCH_SIZE, then
+    WRITE_SIZE): a 256 MiB device copy of known size (reads and writes 256 MiB;
+    it calibrates the counters), then `launches` launches each of the gate+up
+    decode GEMM (M=16, packed codes) and the gate+up prefill GEMM (M=2048),
+    each on a fresh weight copy, one launch per dispatch record."""
+    copy_src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    copy_dst = torch.empty_like(copy_src)
+    copy_dst.copy_(copy_src)
+    torch.cuda.synchronize()
+    for M, case in ((16, synthetic.decode_case), (2048, synthetic.prefill_case)):
+        x, w = case("gate_up", M)
+        x = x.cuda()
+        wq, sw = quantize_rows(w.cuda())
+        ops = quantized_operands(torch, fp8, x)
+        copies = [wq] + [wq.clone() for _ in range(3)]
+        torch.cuda.synchronize()
+        for i in range(launches):
+            fp8.fp8_matmul_quantized(ops[0], ops[1], copies[i % len(copies)], sw, packed_rows=ops[2])
+        torch.cuda.synchronize()
+        del copies
+    print("pmc driver done", flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,6 +209,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--pmc-driver", action="store_true",
+                    help="run only the hardware-counter workload (copy calibration + gate+up GEMMs), no timing")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the FP8 linear path on one GPU; runs on more than one GPU are not part of this build",
@@ -186,6 +225,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP GPU", file=sys.stderr)
         return 2
+    if args.pmc_driver:
+        pmc_driver(torch, fp8, synthetic, quantize_rows)
+        return 0
     b = Bench(torch)
     dev_name = torch.cuda.get_device_name(0)
     M = args.rows
@@ -235,7 +277,8 @@ def main() -> int:
         },
         "roofline": {"bound": "hbm", "kernel": "gemm_decode_kernel (gate+up, N=24576 K=4096, M=16)",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "avg_launch_us": round(k_ms * 1e3, 3), "bytes_per_launch": k_bytes},
+                     "traffic": measured_traffic(f"decode_gate_up_m{M}"), "avg_launch_us": round(k_ms * 1e3, 3),
+                     "bytes_per_launch": k_bytes},
         "decode_kernels": per_shape,
     }
 
@@ -265,6 +308,7 @@ def main() -> int:
             "roofline": {"bound": "mfma", "kernel": "gemm_prefill_kernel (gate+up, N=24576 K=4096, M=2048)",
                          "achieved": round(pk_tf, 1), "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(pk_tf / FP8_PEAK_TFLOPS, 4), "avg_launch_us": round(pk * 1e3, 2),
+                         "traffic": measured_traffic(f"prefill_gate_up_m{Mp}"),
                          "flops_per_launch": 2 * Mp * N * K},
             "kernels": pshape,
         }
