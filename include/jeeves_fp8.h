@@ -99,6 +99,20 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
                   int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, int32_t* tile_counters,
                   int64_t n_counters, void* stream);
 
+/* W8A16 parity mode: the arithmetic of the reference's FP8Linear.forward
+ * (inference/fp8.py:62-99 with its bias at :183-184, stated as
+ * ((x.float() @ w8.float().t()) * scale).to(bf16) in model/metal_test.py:213):
+ *   y[m,n] = bf16( sum_k x[m,k] * w[n,k] * w_scale[n] )   (bf16 x e4m3, fp32 sums)
+ *   then, with a bias, y[m,n] = bf16( y[m,n] + bias[n] ).
+ * No activation quantization: the bf16 activations enter the GEMM as they
+ * are. Arguments as jv_fp8_linear (no LoRA); K a positive multiple of 128.
+ * workspace: jv_w8a16_workspace_bytes(M,N,K) bytes (split-K partials, 0 for
+ * most shapes); tile_counters as jv_fp8_linear. */
+int64_t jv_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int jv_w8a16_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
+                    void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                    int32_t* tile_counters, int64_t n_counters, void* stream);
+
 /* Workspace bytes jv_fp8_gemm needs (split-K partials only). */
 int64_t jv_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 

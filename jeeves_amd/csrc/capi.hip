@@ -206,6 +206,40 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
                   lora_rank, lora_scaling, (uint16_t*)y, ldy, M, N, K, ws, rest, tile_counters, n_counters, s);
 }
 
+int64_t jv_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) { return jv_fp8_gemm_workspace_bytes(M, N, K); }
+
+int jv_w8a16_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
+                    void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                    int32_t* tile_counters, int64_t n_counters, void* stream) {
+  if (int rc = check_gemm_shape(M, N, K)) return rc;
+  if (M == 0) return JV_OK;
+  if (!aligned16(x) || (ldx * 2) % 16 || !aligned16(w) || ldw % 16)
+    return fail(JV_ERR_VALUE, "the W8A16 GEMM needs 16-byte aligned operand rows");
+  if ((uint64_t)N * (uint64_t)ldw >= (1ull << 32) || (uint64_t)M * (uint64_t)ldx * 2 >= (1ull << 32))
+    return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
+  const int cus = cu_count_of(-1);
+  if (cus <= 0) return fail(JV_ERR_HIP, "cannot query the device's compute units");
+  hipStream_t s = (hipStream_t)stream;
+  if (M > jv::kDecodeMaxRows)
+    return hip_status(jv::w8a16_prefill((const uint16_t*)x, ldx, (const uint8_t*)w, ldw, (int)M, (int)N, (int)K, w_scale,
+                                        (const uint16_t*)bias, (uint16_t*)y, ldy, cus, s),
+                      "W8A16 prefill GEMM launch");
+  const jv::DecodePlan plan = jv::decode_plan(M, N, K, cus);
+  float* partial = nullptr;
+  if (plan.splits > 1) {
+    if (!tile_counters || plan.groups > n_counters)
+      return fail(JV_ERR_VALUE, "%lld tiles exceed the %lld tile counters", (long long)plan.groups, (long long)n_counters);
+    const int64_t need = (int64_t)plan.splits * M * N * 4;
+    if (!workspace || workspace_bytes < need)
+      return fail(JV_ERR_VALUE, "workspace too small for split-K partials: %lld < %lld bytes", (long long)workspace_bytes,
+                  (long long)need);
+    partial = reinterpret_cast<float*>(workspace);
+  }
+  return hip_status(jv::w8a16_decode((const uint16_t*)x, ldx, (const uint8_t*)w, ldw, (int)M, (int)N, (int)K, plan, partial,
+                                     tile_counters, w_scale, (const uint16_t*)bias, (uint16_t*)y, ldy, s),
+                    "W8A16 decode GEMM launch");
+}
+
 int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_t ldu, int64_t M, int64_t I, void* codes,
                            int64_t ldc, float* scales, void* h_out, int64_t ldh, const void* lora_a, int64_t lora_rank,
                            float* lora_t, void* stream) {

@@ -179,6 +179,21 @@ __device__ __forceinline__ f32x4 mfma_16x16x128_fp8(i32x8 a, i32x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// 8 e4m3 codes (two dwords) -> 8 bf16 (a 16-byte MFMA operand), in order.
+__device__ __forceinline__ bf16x8 e4m3x8_to_bf16(uint32_t lo, uint32_t hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false), b = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
+  const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, false), d = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, true);
+  // The bf16 value is the upper half of the exact fp32 value.
+  const i32x4 v = {(int)__builtin_amdgcn_perm(__float_as_uint(a.y), __float_as_uint(a.x), 0x07060302),
+                   (int)__builtin_amdgcn_perm(__float_as_uint(b.y), __float_as_uint(b.x), 0x07060302),
+                   (int)__builtin_amdgcn_perm(__float_as_uint(c.y), __float_as_uint(c.x), 0x07060302),
+                   (int)__builtin_amdgcn_perm(__float_as_uint(d.y), __float_as_uint(d.x), 0x07060302)};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
 __device__ __forceinline__ i32x8 cat8(i32x4 lo, i32x4 hi) {
   return i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 }

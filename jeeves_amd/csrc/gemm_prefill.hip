@@ -288,6 +288,184 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
   }
 }
 
+// ---------------------------------------------------------------------------
+// W8A16 parity mode, M > 64: bf16 activations x e4m3 weights (converted to
+// bf16 in registers, exact), v_mfma_f32_32x32x16_bf16, fp32 sums, then
+// y = bf16(acc * sw[n]) and y = bf16(y + bias[n]) -- the reference's own
+// arithmetic (inference/fp8.py:62-99, :183-184; model/metal_test.py:213).
+// Each 64-deep K stage holds BM token rows of 128 B (bf16) and BN weight rows
+// of 64 B (e4m3) in LDS, both swizzled for 16-lane ds_read_b128 phases. A
+// lane half h of the 32x32 operand layout covers k = 32h + [0, 32) of the
+// stage; MFMA q of the stage uses k = 32h + 8q + [0, 8) on both operands.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WGM, int WGN, int STAGES>
+__global__ __launch_bounds__(64 * WGM * WGN) void w8a16_prefill_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw, int M, int N, int K,
+    int tiles_m, int tiles_n, int group_m, const float* __restrict__ sw, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ y, int64_t ldy) {
+  constexpr int NW = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int XROW = 128, WROW = 64;               // bytes per LDS row: 64 bf16, 64 e4m3
+  constexpr int XBYTES = BM * XROW, STAGE = XBYTES + BN * WROW;
+  constexpr int XLOADS = XBYTES / 1024 / NW, WLOADS = BN * WROW / 1024 / NW;
+  constexpr int OUT_CH = BN * 2 / 16;
+  constexpr int LDS_BYTES = STAGES * STAGE > BM * BN * 2 ? STAGES * STAGE : BM * BN * 2;
+  static_assert(XBYTES % (1024 * NW) == 0 && (BN * WROW) % (1024 * NW) == 0 && TM >= 1 && TN >= 1, "tile shape");
+  static_assert(STAGES >= 2 && (STAGES - 2) * (XLOADS + WLOADS) < 64, "pipeline depth");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+
+  int tile_m, tile_n;
+  tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tile_m, tile_n);
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  // DMA assignment: token wave-load g covers rows 8g..8g+7 (lane -> row l/8,
+  // physical chunk l%8 holding logical chunk (l%8) ^ swizzle<128>(row));
+  // weight wave-load g covers rows 16g..16g+15 (lane -> row l/4, chunk l%4).
+  const uint8_t* xsrc[XLOADS];
+  const uint8_t* wsrc[WLOADS];
+#pragma unroll
+  for (int i = 0; i < XLOADS; ++i) {
+    const int r = (i * NW + wave) * 8 + lane / 8;
+    xsrc[i] = reinterpret_cast<const uint8_t*>(x + (int64_t)min(m0 + r, M - 1) * ldx) + ((lane % 8) ^ swizzle<128>(r)) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < WLOADS; ++i) {
+    const int r = (i * NW + wave) * 16 + lane / 4;
+    wsrc[i] = w + (int64_t)min(n0 + r, N - 1) * ldw + ((lane % 4) ^ swizzle<64>(r)) * 16;
+  }
+  auto issue_stage = [&](int kt) {
+    uint8_t* base = lds + (kt % STAGES) * STAGE;
+#pragma unroll
+    for (int i = 0; i < XLOADS; ++i) load_lds16(xsrc[i] + (int64_t)kt * 128, base + (i * NW + wave) * 1024);
+#pragma unroll
+    for (int i = 0; i < WLOADS; ++i) load_lds16(wsrc[i] + (int64_t)kt * 64, base + XBYTES + (i * NW + wave) * 1024);
+  };
+
+  f32x16 acc[TN][TM];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
+
+  const int frow = lane & 31, h = lane >> 5;
+  const int KT = K / 64;
+#pragma unroll
+  for (int p = 0; p < STAGES - 1; ++p)
+    if (p < KT) issue_stage(p);
+  for (int kt = 0; kt < KT; ++kt) {
+    // stage kt has landed once at most min(STAGES-2, KT-1-kt) later stages are in flight
+    const int later = min(STAGES - 2, KT - 1 - kt);
+    if (STAGES > 2 && later >= STAGES - 2) wait_vmem_below<(STAGES > 2 ? (STAGES - 2) * (XLOADS + WLOADS) : 0)>();
+    else if (STAGES > 3 && later == 1) wait_vmem_below<XLOADS + WLOADS>();
+    else wait_vmem_below<0>();
+    barrier_only();
+    // buffer (kt-1) % STAGES was consumed (its MFMAs issued) before the barrier
+    if (kt + STAGES - 1 < KT) issue_stage(kt + STAGES - 1);
+    const uint8_t* base = lds + (kt % STAGES) * STAGE;
+    i32x4 a_raw[TN][2];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int r = wn * WN + j * 32 + frow;
+      const uint8_t* rowp = base + XBYTES + r * WROW;
+      a_raw[j][0] = lds_read16(rowp + ((2 * h) ^ swizzle<64>(r)) * 16);
+      a_raw[j][1] = lds_read16(rowp + ((2 * h + 1) ^ swizzle<64>(r)) * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bf16x8 b[TM];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * WM + i * 32 + frow;
+        b[i] = __builtin_bit_cast(bf16x8, lds_read16(base + r * XROW + ((4 * h + q) ^ swizzle<128>(r)) * 16));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const i32x4 raw = a_raw[j][q >> 1];
+        const bf16x8 a = (q & 1) ? e4m3x8_to_bf16(raw.z, raw.w) : e4m3x8_to_bf16(raw.x, raw.y);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[i], acc[j][i], 0, 0, 0);
+      }
+    }
+  }
+
+  // Epilogue through LDS (as the FP8 kernel): lane l holds token l % 32 and, in
+  // register r, channel 8*(r/4) + 4*(l/32) + r%4.
+  lds_barrier();
+  const bool has_bias = bias != nullptr;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int nl = wn * WN + j * 32 + 8 * qd + 4 * (lane >> 5);
+      uint32_t hv[TM][4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int n = min(n0 + nl + e, N - 1);
+        const float swn = sw[n];
+        const float bn = has_bias ? bf16_to_f32(bias[n]) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          uint32_t v = f32_to_bf16(acc[j][i][4 * qd + e] * swn);
+          if (has_bias) v = f32_to_bf16(bf16_to_f32(v) + bn);
+          hv[i][e] = v;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int ml = wm * WM + i * 32 + (lane & 31);
+        const int chunk = (nl >> 3) ^ (ml % OUT_CH);
+        *reinterpret_cast<uint2*>(lds + ml * (BN * 2) + chunk * 16 + (nl & 4) * 2) =
+            uint2{hv[i][0] | (hv[i][1] << 16), hv[i][2] | (hv[i][3] << 16)};
+      }
+    }
+  }
+  lds_barrier();
+  const bool y_vec = ((ldy | N) & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  for (int c = threadIdx.x; c < BM * OUT_CH; c += 64 * NW) {
+    const int ml = c / OUT_CH, ch = c % OUT_CH;
+    const int m = m0 + ml, n = n0 + ch * 8;
+    if (m >= M || n >= N) continue;
+    const uint4 v = *reinterpret_cast<const uint4*>(lds + ml * (BN * 2) + (ch ^ (ml % OUT_CH)) * 16);
+    uint16_t* dst = y + (int64_t)m * ldy + n;
+    if (y_vec) {
+      *reinterpret_cast<uint4*>(dst) = v;
+    } else {
+      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (n + e < N) dst[e] = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+}
+
+template <int BM, int BN, int WGM, int WGN, int STAGES>
+static hipError_t launch_w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                                       const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy, int group_m,
+                                       hipStream_t stream) {
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  w8a16_prefill_kernel<BM, BN, WGM, WGN, STAGES><<<dim3((unsigned)(tm * tn)), dim3(64 * WGM * WGN), 0, stream>>>(
+      x, ldx, w, ldw, M, N, K, tm, tn, group_m, sw, bias, y, ldy);
+  return hipGetLastError();
+}
+
+hipError_t w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                         const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy, int cu_count,
+                         hipStream_t stream) {
+  if (K % 64) return hipErrorInvalidValue;
+  const int64_t t256 = ((int64_t)(M + 255) / 256) * ((N + 255) / 256);
+  if (t256 >= 2 * (int64_t)cu_count)
+    return launch_w8a16_prefill<256, 256, 2, 4, 3>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 4, stream);
+  const int64_t t128 = ((int64_t)(M + 255) / 256) * ((N + 127) / 128);
+  if (t128 >= cu_count)
+    return launch_w8a16_prefill<256, 128, 2, 4, 3>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 4, stream);
+  return launch_w8a16_prefill<128, 128, 2, 2, 3>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 8, stream);
+}
+
 template <int BM, int BN, int WGM, int WGN, int BK, int STAGES>
 static hipError_t launch_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
                                  const Epilogue& ep, int rank, int group_m, hipStream_t stream) {

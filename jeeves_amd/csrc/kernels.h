@@ -58,4 +58,13 @@ PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count);
 hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
                         const Epilogue& ep, int rank, PrefillTile tile, hipStream_t stream);
 
+// W8A16 parity mode (bf16 activations x e4m3 weights, the reference's own
+// arithmetic): y = bf16(acc * sw[n]), then bf16(y + bias[n]) with a bias.
+hipError_t w8a16_decode(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                        const DecodePlan& p, float* partial, int* counters, const float* sw, const uint16_t* bias,
+                        uint16_t* y, int64_t ldy, hipStream_t stream);
+hipError_t w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                         const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy, int cu_count,
+                         hipStream_t stream);
+
 }  // namespace jv

@@ -1,0 +1,189 @@
+// W8A16 parity mode: the arithmetic the reference's FP8Linear actually runs
+// (inference/fp8.py:62-99, :112-148, stated as ((x.float() @ w8.float().t()) *
+// scale).to(bf16) in model/metal_test.py:213): bf16 activations times e4m3
+// weights, fp32 sums, times the channel scale, rounded to bf16; a bias is
+// added afterwards in bf16 (inference/fp8.py:183-184).
+//
+// On gfx950 the e4m3 weight bytes become bf16 in registers with
+// v_cvt_pk_f32_fp8 (exact: every e4m3 value is a bf16 value) and feed bf16
+// MFMAs with the activations as they are -- no activation quantization, no
+// fp16 detour. Decode (M <= 64) mirrors the FP8 decode kernel: weights are
+// the A side of v_mfma_f32_16x16x32_bf16, each wave streams its k range in
+// bursts straight from HBM, waves meet in LDS, narrow N splits K across
+// workgroups with the same deterministic last-workgroup reduction.
+#include "epilogue.h"
+#include "kernels.h"
+
+namespace jv {
+
+// y = bf16(acc * sw), then bf16(y + bias) when there is a bias: the two
+// roundings of the reference's GEMM output and its separate bias add.
+__device__ __forceinline__ uint16_t w8a16_out(float acc, float swn, const uint16_t* bias, int n) {
+  uint32_t v = f32_to_bf16(acc * swn);
+  if (bias) v = f32_to_bf16(bf16_to_f32(v) + bf16_to_f32(bias[n]));
+  return (uint16_t)v;
+}
+
+// Weights: lane l holds k bytes [32j, 32j+32) of row l%16 for j = l/16 of each
+// 128-k step; the four 16x16x32 MFMAs q of a step use k = 32j + 8q + [0, 8)
+// on both operands.
+template <int MT, int RT, int W, int U>
+__global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                              const uint8_t* __restrict__ w, int64_t ldw, int M, int N,
+                                                              int K, int splits, float* __restrict__ partial,
+                                                              int* __restrict__ counters, const float* __restrict__ sw,
+                                                              const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
+                                                              int64_t ldy) {
+  __shared__ f32x4 red[W][RT * MT][64];
+  __shared__ int is_last;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int group = blockIdx.x, split = blockIdx.y;
+  const int n0 = group * 16 * RT;
+
+  const int ksteps = K >> 7;
+  const int slices = splits * W, slice = split * W + wave;
+  const int s_begin = (int)((int64_t)ksteps * slice / slices), s_end = (int)((int64_t)ksteps * (slice + 1) / slices);
+
+  const int li = lane & 15, j32 = (lane >> 4) * 32;
+  const uint8_t* wp[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) wp[rt] = w + (int64_t)min(n0 + rt * 16 + li, N - 1) * ldw + j32;
+  const uint16_t* xp[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xp[mt] = x + (int64_t)min(mt * 16 + li, M - 1) * ldx + j32;
+
+  f32x4 acc[RT][MT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int s = s_begin; s < s_end; s += U) {
+    i32x4 wa[U][RT][2];
+    i32x4 xa[U][MT][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (s + u >= s_end) break;
+      const int64_t k0 = (int64_t)(s + u) * 128;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        wa[u][rt][0] = *reinterpret_cast<const i32x4*>(wp[rt] + k0);
+        wa[u][rt][1] = *reinterpret_cast<const i32x4*>(wp[rt] + k0 + 16);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xa[u][mt][q] = *reinterpret_cast<const i32x4*>(xp[mt] + k0 + 8 * q);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (s + u >= s_end) break;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const i32x4 w0 = wa[u][rt][0], w1 = wa[u][rt][1];
+        const bf16x8 a[4] = {e4m3x8_to_bf16(w0.x, w0.y), e4m3x8_to_bf16(w0.z, w0.w), e4m3x8_to_bf16(w1.x, w1.y),
+                             e4m3x8_to_bf16(w1.z, w1.w)};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[q], __builtin_bit_cast(bf16x8, xa[u][mt][q]),
+                                                                  acc[rt][mt], 0, 0, 0);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[wave][rt * MT + mt][lane] = acc[rt][mt];
+  __syncthreads();
+
+  // Output (token ml, channel nl) of tile (rt, mt) sits in lane ml + 16*(nl/4),
+  // register nl % 4 (16x16 layout: row = 4*(lane/16) + reg is the channel).
+  const float* redf = reinterpret_cast<const float*>(&red[0][0][0]);
+  constexpr int kOut = RT * MT * 256;
+  for (int idx = threadIdx.x; idx < kOut; idx += 64 * W) {
+    const int t = idx >> 8, rt = t / MT, mt = t % MT, e = idx & 255, ml = e >> 4, nl = e & 15;
+    const int src = (t * 64 + ml + 16 * (nl >> 2)) * 4 + (nl & 3);
+    float sum = 0.0f;
+#pragma unroll
+    for (int wv = 0; wv < W; ++wv) sum += redf[wv * RT * MT * 256 + src];
+    const int m = mt * 16 + ml, n = n0 + rt * 16 + nl;
+    if (m < M && n < N) {
+      if (splits == 1)
+        y[(int64_t)m * ldy + n] = w8a16_out(sum, sw[n], bias, n);
+      else  // device-coherent store: visible to the reducing workgroup without a cache flush
+        __hip_atomic_store(partial + ((int64_t)split * M + m) * N + n, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (splits == 1) return;
+
+  // Every partial store of this workgroup has completed before its count is
+  // added; the workgroup that sees count splits-1 sums all partials in split
+  // order with device-coherent loads and resets the counter.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    is_last = __hip_atomic_fetch_add(counters + group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+  __syncthreads();
+  if (!is_last) return;
+  for (int idx = threadIdx.x; idx < kOut; idx += 64 * W) {
+    const int t = idx >> 8, rt = t / MT, mt = t % MT, e = idx & 255, ml = e >> 4, nl = e & 15;
+    const int m = mt * 16 + ml, n = n0 + rt * 16 + nl;
+    if (m < M && n < N) {
+      float sum = 0.0f;
+      for (int sp = 0; sp < splits; ++sp)
+        sum += __hip_atomic_load(partial + ((int64_t)sp * M + m) * N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      y[(int64_t)m * ldy + n] = w8a16_out(sum, sw[n], bias, n);
+    }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(counters + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Bursts of U steps: the operands of a burst (RT weight tiles, MT token tiles
+// of 32 bf16 per step) stay within the register budget without spilling.
+constexpr int w8a16_unroll(int mt, int rt) { return rt + 2 * mt <= 4 ? 4 : 2; }
+
+template <int MT, int RT, int W>
+static void launch_w8a16_decode(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                                const DecodePlan& p, float* partial, int* counters, const float* sw, const uint16_t* bias,
+                                uint16_t* y, int64_t ldy, hipStream_t stream) {
+  constexpr int U = w8a16_unroll(MT, RT);
+  w8a16_decode_kernel<MT, RT, W, U><<<dim3((unsigned)p.groups, (unsigned)p.splits), dim3(64 * W), 0, stream>>>(
+      x, ldx, w, ldw, M, N, K, p.splits, partial, counters, sw, bias, y, ldy);
+}
+
+template <int MT>
+static void launch_w8a16_decode_mt(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                                   const DecodePlan& p, float* partial, int* counters, const float* sw,
+                                   const uint16_t* bias, uint16_t* y, int64_t ldy, hipStream_t stream) {
+  if (p.rt == 2) {
+    if (p.waves == 8)
+      launch_w8a16_decode<MT, 2, 8>(x, ldx, w, ldw, M, N, K, p, partial, counters, sw, bias, y, ldy, stream);
+    else
+      launch_w8a16_decode<MT, 2, 4>(x, ldx, w, ldw, M, N, K, p, partial, counters, sw, bias, y, ldy, stream);
+  } else {
+    if (p.waves == 8)
+      launch_w8a16_decode<MT, 1, 8>(x, ldx, w, ldw, M, N, K, p, partial, counters, sw, bias, y, ldy, stream);
+    else
+      launch_w8a16_decode<MT, 1, 4>(x, ldx, w, ldw, M, N, K, p, partial, counters, sw, bias, y, ldy, stream);
+  }
+}
+
+hipError_t w8a16_decode(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                        const DecodePlan& p, float* partial, int* counters, const float* sw, const uint16_t* bias,
+                        uint16_t* y, int64_t ldy, hipStream_t stream) {
+  if (M < 1 || M > kDecodeMaxRows || (K & 127)) return hipErrorInvalidValue;
+  switch ((M + 15) / 16) {
+    case 1: launch_w8a16_decode_mt<1>(x, ldx, w, ldw, M, N, K, p, partial, counters, sw, bias, y, ldy, stream); break;
+    case 2: launch_w8a16_decode_mt<2>(x, ldx, w, ldw, M, N, K, p, partial, counters, sw, bias, y, ldy, stream); break;
+    case 3: launch_w8a16_decode_mt<3>(x, ldx, w, ldw, M, N, K, p, partial, counters, sw, bias, y, ldy, stream); break;
+    case 4: launch_w8a16_decode_mt<4>(x, ldx, w, ldw, M, N, K, p, partial, counters, sw, bias, y, ldy, stream); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace jv

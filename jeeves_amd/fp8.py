@@ -133,6 +133,47 @@ def fp8_matmul(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *, bi
     return y
 
 
+def fp8_matmul_w8a16(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *,
+                     bias: torch.Tensor | None = None) -> torch.Tensor:
+    """W8A16 parity mode: the reference's own arithmetic,
+    ``((x.float() @ weight.float().t()) * scale).to(bf16)`` (``model/metal_test.py:213``,
+    ``inference/fp8.py:62-99``), then ``+ bias`` in bf16 (``inference/fp8.py:183-184``).
+
+    The bf16 activations are not quantized; the e4m3 weights are widened to
+    bf16 (exactly) inside the kernel. Same arguments and errors as
+    ``fp8_matmul`` without LoRA.
+    """
+    M, K = x.shape
+    N = weight.shape[0]
+    _check_weight(K, weight)
+    dev = x.device
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    if not _rows_aligned(x, 2):
+        x = x.contiguous()
+    w = weight.view(torch.uint8)
+    if not _rows_aligned(w, 1):
+        w = w.contiguous()
+    y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    if M == 0:
+        return y
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+    scale = scale.to(torch.float32).contiguous()
+    L = _lib.lib()
+    with torch.cuda.device(dev):
+        counters = _tile_counters(dev, M, N, K)
+        ws_bytes = L.jv_w8a16_workspace_bytes(M, N, K)
+        if ws_bytes < 0:
+            _lib.check(_lib.JV_ERR_HIP)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        _lib.check(L.jv_w8a16_linear(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), scale.data_ptr(),
+                                     bias.data_ptr() if bias is not None else None, y.data_ptr(), N, M, N, K,
+                                     ws.data_ptr(), ws_bytes, _lib.counters_ptr(counters),
+                                     counters.numel() if counters is not None else 0, _stream(dev)))
+    return y
+
+
 def packed_codes_bytes(rows: int, cols: int) -> int:
     """Bytes of ``rows x cols`` activation codes in the decode GEMM's packed
     fragment order (rows <= ``DECODE_MAX_ROWS``, cols a multiple of 128)."""
@@ -239,7 +280,15 @@ def swiglu_quantize(gate: torch.Tensor, up: torch.Tensor, *, lora_a: torch.Tenso
 class FP8Linear(nn.Module):
     """``inference/fp8.py:151-185``: buffers ``weight`` (float8_e4m3fn [N,K])
     and ``scale`` (float32 [N]), optional bf16 ``bias``. ``set_lora`` attaches
-    a LoRA adapter (``model/lora.py:122-133``) that the GEMM epilogue adds."""
+    a LoRA adapter (``model/lora.py:122-133``) that the GEMM epilogue adds.
+
+    ``activations`` picks the arithmetic: ``"fp8"`` (default) quantizes the
+    activations per token and runs the FP8 x FP8 GEMM; ``"bf16"`` is the
+    W8A16 parity mode (``fp8_matmul_w8a16``), the reference's own math, for
+    checking a model against the reference's outputs (no LoRA in that mode).
+    """
+
+    ACTIVATIONS = ("fp8", "bf16")
 
     def __init__(self, in_features: int, out_features: int, bias: bool = False, device: torch.device | str | None = None):
         super().__init__()
@@ -248,6 +297,15 @@ class FP8Linear(nn.Module):
         self.bias = nn.Parameter(torch.empty(out_features, dtype=torch.bfloat16, device=device), requires_grad=False) if bias else None
         self.in_features, self.out_features = in_features, out_features
         self.lora: tuple[torch.Tensor, torch.Tensor, float] | None = None
+        self.activations = "fp8"
+
+    def set_activations(self, mode: str) -> None:
+        """``"fp8"`` (per-token e4m3 activations) or ``"bf16"`` (W8A16 parity mode)."""
+        if mode not in self.ACTIVATIONS:
+            raise ValueError(f"activations must be one of {self.ACTIVATIONS}, got {mode!r}")
+        if mode == "bf16" and self.lora is not None:
+            raise ValueError("the W8A16 parity mode has no LoRA epilogue")
+        self.activations = mode
 
     @torch.no_grad()
     def load_codes(self, codes: torch.Tensor, scale: torch.Tensor) -> None:
@@ -261,6 +319,8 @@ class FP8Linear(nn.Module):
     def set_lora(self, a: torch.Tensor, b: torch.Tensor, scaling: float) -> None:
         """Attach ``y += scaling * (x A^T) B^T`` (A [r,in], B [out,r], bf16)."""
         _check_lora((a, b, scaling), self.in_features, self.out_features)
+        if self.activations == "bf16":
+            raise ValueError("the W8A16 parity mode has no LoRA epilogue")
         self.lora = (a.to(torch.bfloat16).contiguous(), b.to(torch.bfloat16).contiguous(), float(scaling))
 
     @classmethod
@@ -277,7 +337,10 @@ class FP8Linear(nn.Module):
         x2 = x.reshape(-1, shape[-1]).to(torch.bfloat16)
         if x2.stride(-1) != 1:
             x2 = x2.contiguous()
-        y = fp8_matmul(x2, self.weight, self.scale, bias=self.bias, lora=self.lora)
+        if self.activations == "bf16":
+            y = fp8_matmul_w8a16(x2, self.weight, self.scale, bias=self.bias)
+        else:
+            y = fp8_matmul(x2, self.weight, self.scale, bias=self.bias, lora=self.lora)
         return y.view(*shape[:-1], self.out_features)
 
 
@@ -297,6 +360,11 @@ class FP8SwiGLU(nn.Module):
         gu = self.gate_up(x.reshape(-1, shape[-1]))
         M = gu.shape[0]
         inter = self.down.in_features
+        if self.down.activations == "bf16":
+            # W8A16 parity mode: h = silu(gate) * up in bf16 feeds the down GEMM as is.
+            h = swiglu_quantize(gu[:, :inter], gu[:, inter:], return_h=True)[-1]
+            y = fp8_matmul_w8a16(h, self.down.weight, self.down.scale, bias=self.down.bias)
+            return y.view(*shape[:-1], self.down.out_features)
         lora_a = self.down.lora[0] if self.down.lora is not None else None
         # Decode batches hand the down GEMM its codes in fragment order.
         packed = 0 < M <= DECODE_MAX_ROWS and inter % BLOCK_K == 0

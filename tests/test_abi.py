@@ -25,7 +25,7 @@ def declared_functions() -> set[str]:
 def test_header_declares_the_path():
     names = declared_functions()
     for required in ("jv_fp8_linear", "jv_fp8_gemm", "jv_fp8_quantize_rows_bf16", "jv_fp8_quantize_rows_f32",
-                     "jv_fp8_swiglu_quantize", "jv_device_cu_count", "jv_fp8_last_error"):
+                     "jv_fp8_swiglu_quantize", "jv_device_cu_count", "jv_fp8_last_error", "jv_w8a16_linear"):
         assert required in names
 
 
@@ -56,7 +56,12 @@ def test_value_errors_need_no_device(product_lib):
     assert rc == _lib.JV_ERR_VALUE and b"rank 8" in L.jv_fp8_last_error()
     rc = L.jv_fp8_swiglu_quantize(None, 0, None, 0, 4, 20000, None, 0, None, None, 0, None, 0, None, None)
     assert rc == _lib.JV_ERR_VALUE
+    rc = L.jv_w8a16_linear(None, 0, None, 0, None, None, None, 0, 4, 64, 100, None, 0, None, 0, None)
+    assert rc == _lib.JV_ERR_VALUE and b"divisible by 128" in L.jv_fp8_last_error()
+    rc = L.jv_w8a16_linear(None, 3, None, 0, None, None, None, 0, 4, 64, 128, None, 0, None, 0, None)
+    assert rc == _lib.JV_ERR_VALUE and b"aligned" in L.jv_fp8_last_error()
     # M = 0 is a no-op that succeeds
+    assert L.jv_w8a16_linear(None, 0, None, 0, None, None, None, 0, 0, 64, 128, None, 0, None, 0, None) == 0
     assert L.jv_fp8_linear(None, 0, None, 0, None, None, None, None, 0, 0.0, None, 0, 0, 64, 128, None, 0, None, 0, None) == 0
 
 
