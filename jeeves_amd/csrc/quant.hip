@@ -1,63 +1,17 @@
-// Per-row e4m3fn quantizer on gfx950: the arithmetic of quantize_rows
-// (inference/fp8_weights.py:16-19) applied to token rows of the activations
-// (and to weight rows at load time).
-//
-//   scale[m] = max(amax_k |x[m,k]|, 1e-12) * fp32(1/448)
-//   code[m,k] = e4m3fn_rne(x[m,k] / scale[m])        (IEEE fp32 quotient)
-//
-// One 256-thread workgroup per row. Each thread owns 8-element chunks
-// c = tid + i*256 and keeps them in registers between the amax pass and the
-// encode pass, so HBM sees each input byte once. The row maximum is taken on
-// the 15-bit bf16 magnitude patterns with packed 16-bit integer max, which is
-// exact and propagates NaN (NaN patterns sort above inf).
-//
-// Variants:
-//   * SWIGLU: the row is h = bf16(bf16(silu(gate)) * up) (model/model.py:583),
-//     built on the fly from the gate and up halves of a fused projection.
-//   * RANK > 0: also emits the LoRA down-projection t[m,r] = sum_k x[m,k] A[r,k]
-//     (model/lora.py:128-131) in fp32 from the same registers.
-#include "fp8_common.h"
-#include "kernels.h"
+// Per-row e4m3fn quantizer kernels on gfx950 (quantize_rows,
+// inference/fp8_weights.py:16-19, on token rows of the activations and on
+// weight rows at load time): one workgroup per row running quant_row
+// (quant_row.h) with one or two 8-element chunks per thread -- 512 threads
+// up to K = 4096, 1024 above (the encode is on each thread's critical path:
+// measured 4.9 us with 256 threads vs 3.3 us with 1024 at K = 12288, 16
+// rows) -- a two-pass kernel for rows longer than 16384, and an fp32-row
+// kernel for weights handed over in fp32.
+#include "quant_row.h"
 
 namespace jv {
 
+// Threads of the two-pass and fp32 kernels.
 constexpr int kQuantThreads = 256;
-
-// silu in fp32 rounded to bf16, times up, rounded to bf16.
-__device__ __forceinline__ uint32_t swiglu_bf16(uint32_t g16, uint32_t u16) {
-  const float g = bf16_to_f32(g16);
-  const float s = g / (1.0f + expf(-g));
-  const float sb = bf16_to_f32(f32_to_bf16(s));
-  return f32_to_bf16(sb * bf16_to_f32(u16));
-}
-
-__device__ __forceinline__ uint32_t swiglu_pair(uint32_t g2, uint32_t u2) {
-  return swiglu_bf16(g2 & 0xFFFFu, u2 & 0xFFFFu) | (swiglu_bf16(g2 >> 16, u2 >> 16) << 16);
-}
-
-template <int RANK>
-__device__ __forceinline__ void lora_accumulate(float (&t)[RANK > 0 ? RANK : 1], uint4 v, const uint16_t* __restrict__ a,
-                                                int64_t K, int c) {
-  if constexpr (RANK > 0) {
-    float f[8];
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      f[2 * j] = bf16_to_f32(w[j] & 0xFFFFu);
-      f[2 * j + 1] = bf16_to_f32(w[j] >> 16);
-    }
-#pragma unroll
-    for (int r = 0; r < RANK; ++r) {
-      const uint4 av = *reinterpret_cast<const uint4*>(a + r * K + (int64_t)c * 8);
-      const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        t[r] = __builtin_fmaf(f[2 * j], bf16_to_f32(aw[j] & 0xFFFFu), t[r]);
-        t[r] = __builtin_fmaf(f[2 * j + 1], bf16_to_f32(aw[j] >> 16), t[r]);
-      }
-    }
-  }
-}
 
 // Block-wide max of a per-thread 15-bit magnitude.
 __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
@@ -65,81 +19,20 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) red[wave] = v;
   __syncthreads();
-  v = max(max(red[0], red[1]), max(red[2], red[3]));
+  v = red[0];
+  for (int i = 1; i < kQuantThreads / 64; ++i) v = max(v, red[i]);
   return v;
 }
 
-// NC: chunks of 8 elements per thread kept in registers (K <= NC * 2048).
-// PACKED: codes go to the packed decode layout (packed_x_offset); the grid
-// then also covers the padding rows M..16*ceil(M/16)-1, which get zero codes.
-template <int NC, bool SWIGLU, int RANK, bool PACKED>
-__global__ __launch_bounds__(kQuantThreads) void quant_rows_bf16_kernel(
+// NC chunks of 8 elements per thread kept in registers (K <= NC * 8 * THREADS).
+template <int THREADS, int NC, bool SWIGLU, int RANK, bool PACKED>
+__global__ __launch_bounds__(THREADS) void quant_rows_bf16_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ up, int64_t ldu, int K, int M,
     uint8_t* __restrict__ codes, int64_t ldc, float* __restrict__ scales, uint16_t* __restrict__ h_out, int64_t ldh,
     const uint16_t* __restrict__ lora_a, float* __restrict__ lora_t) {
-  __shared__ uint32_t red[4];
-  __shared__ float tred[4][RANK > 0 ? RANK : 1];
-  const int64_t row = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int nchunks = K >> 3;
-  if (PACKED && row >= M) {
-    for (int c = tid; c < nchunks; c += kQuantThreads)
-      *reinterpret_cast<uint2*>(codes + packed_x_offset((int)row, c * 8, K >> 7)) = uint2{0u, 0u};
-    return;
-  }
-  const uint16_t* xr = x + row * ldx;
-  uint4 v[NC];
-  uint32_t am = 0;
-  float t[RANK > 0 ? RANK : 1];
-#pragma unroll
-  for (int r = 0; r < (RANK > 0 ? RANK : 1); ++r) t[r] = 0.0f;
-
-#pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int c = tid + i * kQuantThreads;
-    if (c < nchunks) {
-      if constexpr (SWIGLU) {
-        const uint4 g = *reinterpret_cast<const uint4*>(xr + (int64_t)c * 8);
-        const uint4 u = *reinterpret_cast<const uint4*>(up + row * ldu + (int64_t)c * 8);
-        v[i] = uint4{swiglu_pair(g.x, u.x), swiglu_pair(g.y, u.y), swiglu_pair(g.z, u.z), swiglu_pair(g.w, u.w)};
-        if (h_out) *reinterpret_cast<uint4*>(h_out + row * ldh + (int64_t)c * 8) = v[i];
-      } else {
-        v[i] = *reinterpret_cast<const uint4*>(xr + (int64_t)c * 8);
-      }
-      am = pk_max_u16(am, v[i].x & 0x7FFF7FFFu);
-      am = pk_max_u16(am, v[i].y & 0x7FFF7FFFu);
-      am = pk_max_u16(am, v[i].z & 0x7FFF7FFFu);
-      am = pk_max_u16(am, v[i].w & 0x7FFF7FFFu);
-      lora_accumulate<RANK>(t, v[i], lora_a, K, c);
-    } else {
-      v[i] = uint4{0, 0, 0, 0};
-    }
-  }
-  am = max(am & 0xFFFFu, am >> 16);
-  const uint32_t amax_bits = block_max(am, red);
-  const float scale = scale_from_amax_bits(amax_bits);
-  if (tid == 0) scales[row] = scale;
-  const bool fast = amax_bits < 0x7F80u;  // finite row: scale finite and > 0
-  const float r = 1.0f / scale;
-  uint8_t* cr = codes + (PACKED ? 0 : row * ldc);
-#pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int c = tid + i * kQuantThreads;
-    if (c < nchunks) {
-      const int64_t off = PACKED ? packed_x_offset((int)row, c * 8, K >> 7) : (int64_t)c * 8;
-      *reinterpret_cast<uint2*>(cr + off) = encode8(v[i], scale, r, fast);
-    }
-  }
-  if constexpr (RANK > 0) {
-    const int lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-    for (int q = 0; q < RANK; ++q) {
-      const float s = wave_sum_f32(t[q]);
-      if (lane == 0) tred[wave][q] = s;
-    }
-    __syncthreads();
-    if (tid < RANK) lora_t[row * RANK + tid] = (tred[0][tid] + tred[1][tid]) + (tred[2][tid] + tred[3][tid]);
-  }
+  __shared__ uint32_t lds[quant_row_lds_bytes<THREADS, RANK>() / 4];
+  quant_row<THREADS, NC, SWIGLU, RANK, PACKED>((int)blockIdx.x, x, ldx, up, ldu, K, M, codes, ldc, scales, h_out, ldh,
+                                               lora_a, lora_t, lds);
 }
 
 // Rows longer than the register cache: two passes over the row (the second
@@ -147,7 +40,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_bf16_kernel(
 __global__ __launch_bounds__(kQuantThreads) void quant_rows_bf16_long_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                              int K, uint8_t* __restrict__ codes, int64_t ldc,
                                                                              float* __restrict__ scales) {
-  __shared__ uint32_t red[4];
+  __shared__ uint32_t red[kQuantThreads / 64];
   const int64_t row = blockIdx.x;
   const int nchunks = K >> 3;
   const uint16_t* xr = x + row * ldx;
@@ -177,7 +70,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_bf16_long_kernel(con
 __global__ __launch_bounds__(kQuantThreads) void quant_rows_f32_kernel(const float* __restrict__ x, int64_t ldx, int K,
                                                                        uint8_t* __restrict__ codes, int64_t ldc,
                                                                        float* __restrict__ scales) {
-  __shared__ float red[4];
+  __shared__ float red[kQuantThreads / 64];
   const int64_t row = blockIdx.x;
   const float* xr = x + row * ldx;
   float am = 0.0f;
@@ -197,7 +90,8 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_f32_kernel(const flo
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) red[wave] = __uint_as_float(bits);
   __syncthreads();
-  bits = max(max(__float_as_uint(red[0]), __float_as_uint(red[1])), max(__float_as_uint(red[2]), __float_as_uint(red[3])));
+  bits = __float_as_uint(red[0]);
+  for (int i = 1; i < kQuantThreads / 64; ++i) bits = max(bits, __float_as_uint(red[i]));
   const float scale = scale_from_amax_f32(__uint_as_float(bits));
   if (threadIdx.x == 0) scales[row] = scale;
   for (int k = threadIdx.x * 4; k < K; k += kQuantThreads * 4) {
@@ -208,38 +102,38 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_f32_kernel(const flo
   }
 }
 
+// Register-path shape for rows of K elements: 1 = 512 threads x 1 chunk
+// (K <= 4096), 2 = 1024 x 1 (K <= 8192), 3 = 1024 x 2 (K <= 16384); 0 when
+// the row needs the two-pass kernel.
+int quant_chunks(int K) {
+  if (K <= 4096) return 1;
+  if (K <= 8192) return 2;
+  if (K <= 16384) return 3;
+  return 0;
+}
+
 template <bool SWIGLU, int RANK, bool PACKED = false>
-static hipError_t launch_rows(int NC, const uint16_t* x, int64_t ldx, const uint16_t* up, int64_t ldu, int64_t M, int K,
+static hipError_t launch_rows(int shape, const uint16_t* x, int64_t ldx, const uint16_t* up, int64_t ldu, int64_t M, int K,
                               uint8_t* codes, int64_t ldc, float* scales, uint16_t* h_out, int64_t ldh,
                               const uint16_t* lora_a, float* lora_t, hipStream_t stream) {
-  const dim3 grid((unsigned)(PACKED ? (M + 15) / 16 * 16 : M)), block(kQuantThreads);
-#define JV_QUANT_CASE(n)                                                                                              \
-  case n:                                                                                                             \
-    quant_rows_bf16_kernel<n, SWIGLU, RANK, PACKED>                                                                  \
-        <<<grid, block, 0, stream>>>(x, ldx, up, ldu, K, (int)M, codes, ldc, scales, h_out, ldh, lora_a, lora_t);   \
-    break;
-  switch (NC) {
-    JV_QUANT_CASE(1)
-    JV_QUANT_CASE(2)
-    JV_QUANT_CASE(3)
-    JV_QUANT_CASE(4)
-    JV_QUANT_CASE(6)
-    JV_QUANT_CASE(8)
+  const dim3 grid((unsigned)(PACKED ? (M + 15) / 16 * 16 : M));
+  switch (shape) {
+    case 1:
+      quant_rows_bf16_kernel<512, 1, SWIGLU, RANK, PACKED>
+          <<<grid, dim3(512), 0, stream>>>(x, ldx, up, ldu, K, (int)M, codes, ldc, scales, h_out, ldh, lora_a, lora_t);
+      break;
+    case 2:
+      quant_rows_bf16_kernel<1024, 1, SWIGLU, RANK, PACKED>
+          <<<grid, dim3(1024), 0, stream>>>(x, ldx, up, ldu, K, (int)M, codes, ldc, scales, h_out, ldh, lora_a, lora_t);
+      break;
+    case 3:
+      quant_rows_bf16_kernel<1024, 2, SWIGLU, RANK, PACKED>
+          <<<grid, dim3(1024), 0, stream>>>(x, ldx, up, ldu, K, (int)M, codes, ldc, scales, h_out, ldh, lora_a, lora_t);
+      break;
     default:
       return hipErrorInvalidValue;
   }
-#undef JV_QUANT_CASE
   return hipGetLastError();
-}
-
-// Register-cache depth for a row of K elements, or 0 when the row needs the
-// two-pass kernel.
-int quant_chunks(int K) {
-  const int nc = (K + 8 * kQuantThreads - 1) / (8 * kQuantThreads);
-  if (nc <= 4) return nc < 1 ? 1 : nc;
-  if (nc <= 6) return 6;
-  if (nc <= 8) return 8;
-  return 0;
 }
 
 hipError_t quant_rows_bf16(const uint16_t* x, int64_t ldx, int64_t M, int K, uint8_t* codes, int64_t ldc, float* scales,
