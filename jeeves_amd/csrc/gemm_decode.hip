@@ -21,6 +21,8 @@
 //     the last workgroup of a tile (device-scope counter) sums them in split
 //     order and resets the counter -- one launch, deterministic, no cache
 //     flushes, capture-safe.
+#include <type_traits>
+
 #include "epilogue.h"
 #include "kernels.h"
 
@@ -61,12 +63,16 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int s = s_begin; s < s_end; s += UNROLL) {
+  // One burst of up to UNROLL k steps: all its loads are issued, then the
+  // MFMAs consume them. A full burst is straight-line code, so each step's
+  // MFMAs wait only for that step's data; a short last burst guards each step.
+  auto burst = [&](int s, auto full) {
+    constexpr bool FULL = decltype(full)::value;
     i32x4 wa[UNROLL][RT][2];
     i32x4 xa[UNROLL][MT][2];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      if (s + u >= s_end) break;
+      if (!FULL && s + u >= s_end) break;
       const int64_t off = (int64_t)(s + u) * 128;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
@@ -80,9 +86,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
         xa[u][mt][1] = *reinterpret_cast<const i32x4*>(xp[mt] + xo + (PACKX ? 1024 : 16));
       }
     }
+    if constexpr (FULL) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      if (s + u >= s_end) break;
+      if (!FULL && s + u >= s_end) break;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const i32x8 b = cat8(xa[u][mt][0], xa[u][mt][1]);
@@ -90,7 +97,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
         for (int rt = 0; rt < RT; ++rt) acc[rt][mt] = mfma_16x16x128_fp8(cat8(wa[u][rt][0], wa[u][rt][1]), b, acc[rt][mt]);
       }
     }
-  }
+  };
+  int s = s_begin;
+  for (; s + UNROLL <= s_end; s += UNROLL) burst(s, std::true_type{});
+  if (s < s_end) burst(s, std::false_type{});
 
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
