@@ -101,12 +101,16 @@ class Bench:
 
 
 def build_set(torch, synthetic, quantize_rows, M: int, case):
-    """Quantized weights (rotated copies) and bf16 activations for one workload."""
+    """Quantized weights (rotated copies) and bf16 activations for one
+    workload. The codes are stored as FP8Linear stores them for these shapes:
+    in the tiled layout (tile_weight)."""
+    from jeeves_amd.fp8 import tile_weight
+
     weights, xs = {}, {}
     for name in synthetic.SHAPES:
         x, w = case(name, M)
         wq, sw = quantize_rows(w.cuda())
-        weights[name] = (wq, sw)
+        weights[name] = (tile_weight(wq), sw)
         xs[name] = x.cuda()
     per_copy = sum(wq.numel() for wq, _ in weights.values())
     copies = max(2, -(-ROTATE_BYTES // per_copy) + 1)
@@ -142,7 +146,7 @@ def kernel_ms(b: Bench, fp8, rot, operands, name: str, replays: int) -> float:
         def launches(c=c):
             for j in range(LAUNCHES_PER_GRAPH):
                 wq, sw = rot[(c + j) % len(rot)][name]
-                fp8.fp8_matmul_quantized(xq, sx, wq, sw, packed_rows=packed_rows)
+                fp8.fp8_matmul_quantized(xq, sx, wq, sw, packed_rows=packed_rows, tiled=True)
         graphs.append(b.capture(launches))
     return b.time_graphs(graphs, replays, 3) / LAUNCHES_PER_GRAPH
 
@@ -189,11 +193,12 @@ def pmc_driver(torch, fp8, synthetic, quantize_rows, launches: int = 10) -> None
         x, w = case("gate_up", M)
         x = x.cuda()
         wq, sw = quantize_rows(w.cuda())
+        wq = fp8.tile_weight(wq)
         ops = quantized_operands(torch, fp8, x)
         copies = [wq] + [wq.clone() for _ in range(3)]
         torch.cuda.synchronize()
         for i in range(launches):
-            fp8.fp8_matmul_quantized(ops[0], ops[1], copies[i % len(copies)], sw, packed_rows=ops[2])
+            fp8.fp8_matmul_quantized(ops[0], ops[1], copies[i % len(copies)], sw, packed_rows=ops[2], tiled=True)
         torch.cuda.synchronize()
         del copies
     print("pmc driver done", flush=True)
@@ -238,7 +243,7 @@ def main() -> int:
     def step(c):
         for name in synthetic.SHAPES:
             wq, sw = rot[c][name]
-            fp8.fp8_matmul(xs[name], wq, sw)
+            fp8.fp8_matmul(xs[name], wq, sw, tiled=True)
 
     graphs = [b.capture(lambda c=c: step(c)) for c in range(copies)]
     ms = b.time_graphs(graphs, args.steps, args.warmup)
@@ -271,7 +276,8 @@ def main() -> int:
         "config": {
             "workload": f"decode M={M}: 9B-class FP8 linears q 4096->4096, k/v 4096->1024, o 4096->4096, gate+up "
                         f"4096->24576, down 12288->4096, one pass each per step (quant + GEMM + epilogue) replayed as "
-                        f"a HIP graph, weights rotated over {copies} copies ({copies * per_copy / 2**20:.0f} MiB)",
+                        f"a HIP graph, weights in FP8Linear's tiled layout rotated over {copies} copies "
+                        f"({copies * per_copy / 2**20:.0f} MiB)",
             "tokens": M,
             "device": dev_name,
         },
@@ -293,7 +299,7 @@ def main() -> int:
         def pstep(c):
             for name in synthetic.SHAPES:
                 wq, sw = prot[c][name]
-                fp8.fp8_matmul(pxs[name], wq, sw)
+                fp8.fp8_matmul(pxs[name], wq, sw, tiled=True)
 
         pgraphs = [b.capture(lambda c=c: pstep(c)) for c in range(pcopies)]
         pms = b.time_graphs(pgraphs, max(args.steps // 8, 20), 3)

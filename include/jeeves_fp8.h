@@ -84,7 +84,8 @@ int64_t jv_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t l
  *   y[m,n] = bf16( acc[m,n] * sx[m] * w_scale[n] + bias[n]
  *                  + lora_scaling * sum_r (x A^T)[m,r] * B[n,r] ),
  *   acc[m,n] = sum_k xq[m,k] * w[n,k]  (e4m3 x e4m3, fp32 accumulation).
- * x: [M,K] bf16 (row stride ldx); w: [N,K] e4m3fn (row stride ldw);
+ * x: [M,K] bf16 (row stride ldx); w: [N,K] e4m3fn (row stride ldw, or
+ * ldw = 0: the tiled layout below);
  * w_scale: [N] fp32; bias: [N] bf16 or NULL; lora_a: [rank,K] bf16 and
  * lora_b: [N,rank] bf16, or NULL with lora_rank 0 (rank 16 supported);
  * y: [M,N] bf16 (row stride ldy).
@@ -138,6 +139,21 @@ int jv_fp8_gemm(const void* xq, int64_t ldxq, const float* x_scale, const void* 
 int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_t ldu, int64_t M, int64_t I, void* codes,
                            int64_t ldc, float* scales, void* h_out, int64_t ldh, const void* lora_a, int64_t lora_rank,
                            float* lora_t, void* stream);
+
+/* Tiled weight layout. Every GEMM entry point takes ldw = 0 to mean that w
+ * holds the codes in the decode MFMA's fragment order instead of row-major:
+ * for 16-row tile t = n/16 and 128-deep step s = k/128, a 2 KB fragment of
+ * two 1 KB halves (h = (k%32)/16), each 64 lanes x 16 bytes with
+ * lane = n%16 + 16*((k%128)/32); byte offset
+ *   ((t*(K/128) + s)*2 + h)*1024 + lane*16 + k%16.
+ * It needs N % 16 == 0 and K % 128 == 0 and holds N*K bytes; decode waves
+ * read it as one contiguous 1 KB per load. No counterpart in the reference's
+ * CUDA path; its Metal path stores its weights tiled for its own kernel in
+ * the same way (MetalFP8Linear.tiled_codes, inference/fp8_metal.py:13-34;
+ * tile_fp8_codes, model/metal.py:705). These convert codes (row stride ldc)
+ * to and from it, asynchronously on `stream`; not in place. */
+int jv_fp8_tile_weight(const void* codes, int64_t ldc, int64_t N, int64_t K, void* tiled, void* stream);
+int jv_fp8_untile_weight(const void* tiled, int64_t N, int64_t K, void* codes, int64_t ldc, void* stream);
 
 /* Dispatch introspection (the role of split_for, inference/fp8.py:105-109):
  * the number of K splits across workgroups the GEMM uses for these sizes on a

@@ -35,6 +35,8 @@ SIGNATURES: dict[str, tuple] = {
     "jv_w8a16_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64]),
     "jv_w8a16_linear": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64,
                                 c_int64, c_void_p, c_int64, POINTER(c_int32), c_int64, c_void_p]),
+    "jv_fp8_tile_weight": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
+    "jv_fp8_untile_weight": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p]),
     "jv_fp8_split_for": (c_int, [c_int64, c_int64, c_int64, c_int]),
     "jv_fp8_counters_needed": (c_int64, [c_int64, c_int64, c_int64, c_int]),
 }

@@ -71,8 +71,7 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, co
              int32_t* counters, int64_t n_counters, hipStream_t stream) {
   const int cus = cu_count_of(-1);
   if (cus <= 0) return fail(JV_ERR_HIP, "cannot query the device's compute units");
-  if ((uint64_t)N * (uint64_t)ldw >= (1ull << 32) || (uint64_t)M * (uint64_t)ldxq >= (1ull << 32))
-    return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
+  if ((uint64_t)M * (uint64_t)ldxq >= (1ull << 32)) return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
   jv::Epilogue ep{sx, sw, bias, lora_t, lora_b, lora_scaling, y, ldy};
   if (M <= jv::kDecodeMaxRows) {
     const jv::DecodePlan plan = jv::decode_plan(M, N, K, cus);
@@ -95,6 +94,20 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, co
   const jv::PrefillTile tile = jv::prefill_tile(M, N, cus);
   return hip_status(jv::gemm_prefill(xq, ldxq, w, ldw, (int)M, (int)N, (int)K, ep, (int)rank, tile, stream),
                     "fp8 prefill GEMM launch");
+}
+
+// ldw = 0 selects the tiled weight layout (tiled_w_offset), which needs
+// whole 16-row tiles; a row-major ldw must cover a row.
+int check_weight(int64_t N, int64_t K, int64_t ldw, const void* w) {
+  if (!aligned16(w)) return fail(JV_ERR_VALUE, "weight codes must be 16-byte aligned");
+  if (ldw == 0) {
+    if (N % 16) return fail(JV_ERR_VALUE, "tiled weights need out_features divisible by 16, got %lld", (long long)N);
+    if ((uint64_t)N * (uint64_t)K >= (1ull << 32)) return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
+    return JV_OK;
+  }
+  if (ldw % 16 || ldw < K) return fail(JV_ERR_VALUE, "weight row stride %lld must be a multiple of 16 and >= K", (long long)ldw);
+  if ((uint64_t)N * (uint64_t)ldw >= (1ull << 32)) return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
+  return JV_OK;
 }
 
 int check_lora(int64_t rank, const void* a_or_t, const void* b) {
@@ -166,8 +179,8 @@ int jv_fp8_gemm(const void* xq, int64_t ldxq, const float* x_scale, const void* 
   const bool packed = ldxq == 0;
   if (packed && M > jv::kDecodeMaxRows)
     return fail(JV_ERR_VALUE, "packed activation codes hold at most %d rows, got %lld", jv::kDecodeMaxRows, (long long)M);
-  if (!aligned16(xq) || ldxq % 16 || !aligned16(w) || ldw % 16)
-    return fail(JV_ERR_VALUE, "the fp8 GEMM needs 16-byte aligned operand rows");
+  if (!aligned16(xq) || ldxq % 16) return fail(JV_ERR_VALUE, "the fp8 GEMM needs 16-byte aligned operand rows");
+  if (int rc = check_weight(N, K, ldw, w)) return rc;
   return run_gemm((const uint8_t*)xq, ldxq, packed, x_scale, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t,
                   (const uint16_t*)lora_b, lora_rank, lora_scaling, (uint16_t*)y, ldy, M, N, K, (uint8_t*)workspace,
                   workspace_bytes, tile_counters, n_counters, (hipStream_t)stream);
@@ -180,8 +193,8 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
   if (int rc = check_gemm_shape(M, N, K)) return rc;
   if (int rc = check_lora(lora_rank, lora_a, lora_b)) return rc;
   if (M == 0) return JV_OK;
-  if (!aligned16(x) || (ldx * 2) % 16 || !aligned16(w) || ldw % 16)
-    return fail(JV_ERR_VALUE, "the fp8 GEMM needs 16-byte aligned operand rows");
+  if (!aligned16(x) || (ldx * 2) % 16) return fail(JV_ERR_VALUE, "the fp8 GEMM needs 16-byte aligned operand rows");
+  if (int rc = check_weight(N, K, ldw, w)) return rc;
   if (lora_rank && jv::quant_chunks((int)K) == 0)
     return fail(JV_ERR_VALUE, "LoRA needs in_features <= 16384, got %lld", (long long)K);
   const int64_t need = jv_fp8_linear_workspace_bytes(M, N, K, lora_rank);
@@ -213,10 +226,9 @@ int jv_w8a16_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, cons
                     int32_t* tile_counters, int64_t n_counters, void* stream) {
   if (int rc = check_gemm_shape(M, N, K)) return rc;
   if (M == 0) return JV_OK;
-  if (!aligned16(x) || (ldx * 2) % 16 || !aligned16(w) || ldw % 16)
-    return fail(JV_ERR_VALUE, "the W8A16 GEMM needs 16-byte aligned operand rows");
-  if ((uint64_t)N * (uint64_t)ldw >= (1ull << 32) || (uint64_t)M * (uint64_t)ldx * 2 >= (1ull << 32))
-    return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
+  if (!aligned16(x) || (ldx * 2) % 16) return fail(JV_ERR_VALUE, "the W8A16 GEMM needs 16-byte aligned operand rows");
+  if (int rc = check_weight(N, K, ldw, w)) return rc;
+  if ((uint64_t)M * (uint64_t)ldx * 2 >= (1ull << 32)) return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
   const int cus = cu_count_of(-1);
   if (cus <= 0) return fail(JV_ERR_HIP, "cannot query the device's compute units");
   hipStream_t s = (hipStream_t)stream;
@@ -258,6 +270,28 @@ int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_
                                           ldc, scales, (uint16_t*)h_out, ldh, (const uint16_t*)lora_a, (int)lora_rank,
                                           lora_t, packed, (hipStream_t)stream),
                     "swiglu_quantize launch");
+}
+
+int jv_fp8_tile_weight(const void* codes, int64_t ldc, int64_t N, int64_t K, void* tiled, void* stream) {
+  if (N < 0 || N % 16 || K <= 0 || K % JV_FP8_BLOCK_K || N > INT32_MAX || K > INT32_MAX)
+    return fail(JV_ERR_VALUE, "tiling needs N divisible by 16 and K by %d, got N=%lld K=%lld", JV_FP8_BLOCK_K, (long long)N,
+                (long long)K);
+  if (!aligned16(codes) || !aligned16(tiled) || ldc % 16 || ldc < K)
+    return fail(JV_ERR_VALUE, "tiling needs 16-byte aligned rows");
+  if (codes == tiled) return fail(JV_ERR_VALUE, "tiling cannot run in place");
+  return hip_status(jv::tile_weight((const uint8_t*)codes, ldc, (int)N, (int)K, (uint8_t*)tiled, (hipStream_t)stream),
+                    "weight tiling launch");
+}
+
+int jv_fp8_untile_weight(const void* tiled, int64_t N, int64_t K, void* codes, int64_t ldc, void* stream) {
+  if (N < 0 || N % 16 || K <= 0 || K % JV_FP8_BLOCK_K || N > INT32_MAX || K > INT32_MAX)
+    return fail(JV_ERR_VALUE, "untiling needs N divisible by 16 and K by %d, got N=%lld K=%lld", JV_FP8_BLOCK_K, (long long)N,
+                (long long)K);
+  if (!aligned16(codes) || !aligned16(tiled) || ldc % 16 || ldc < K)
+    return fail(JV_ERR_VALUE, "untiling needs 16-byte aligned rows");
+  if (codes == tiled) return fail(JV_ERR_VALUE, "untiling cannot run in place");
+  return hip_status(jv::untile_weight((const uint8_t*)tiled, (int)N, (int)K, (uint8_t*)codes, ldc, (hipStream_t)stream),
+                    "weight untiling launch");
 }
 
 int jv_fp8_split_for(int64_t M, int64_t N, int64_t K, int cu_count) {

@@ -1,4 +1,7 @@
 // Small-M FP8 x FP8 GEMM (decode: M <= 64 tokens), HBM-bound on the weights.
+// Weights come row-major (ldw > 0) or in the tiled fragment layout (ldw = 0,
+// tiled_w_offset), which turns each wave's weight load into one contiguous
+// 1 KB (measured 2-29 % faster over the 9B projection shapes).
 //
 // Counterpart of _fp8_matmul's split-K regime (inference/fp8.py:62-99,
 // :118-123), redesigned for CDNA4:
@@ -28,7 +31,7 @@
 
 namespace jv {
 
-template <int MT, int RT, int WAVES, int UNROLL, bool PACKX, int RANK>
+template <int MT, int RT, int WAVES, int UNROLL, bool PACKX, int RANK, bool PACKW>
 __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* __restrict__ xq, int64_t ldxq,
                                                                  const uint8_t* __restrict__ w, int64_t ldw, int M, int N,
                                                                  int K, int splits, float* __restrict__ partial,
@@ -49,9 +52,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
 
   const int li = lane & 15;
   const int lk = (lane >> 4) * 32;
+  // Weights: row-major rows (lane -> row n0 + 16 rt + l%16, 32 bytes at k =
+  // 32 (l/16)), or the tiled layout (lane -> 16 contiguous bytes of each
+  // 1 KB half of the tile's 2 KB step fragment).
   const uint8_t* wp[RT];
+  const int ntiles = (N + 15) >> 4;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) wp[rt] = w + (int64_t)min(n0 + rt * 16 + li, N - 1) * ldw + lk;
+  for (int rt = 0; rt < RT; ++rt)
+    wp[rt] = PACKW ? w + (int64_t)min(group * RT + rt, ntiles - 1) * ksteps * 2048 + lane * 16
+                   : w + (int64_t)min(n0 + rt * 16 + li, N - 1) * ldw + lk;
   const uint8_t* xp[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -74,10 +83,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
     for (int u = 0; u < UNROLL; ++u) {
       if (!FULL && s + u >= s_end) break;
       const int64_t off = (int64_t)(s + u) * 128;
+      const int64_t woff = PACKW ? (int64_t)(s + u) * 2048 : off;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        wa[u][rt][0] = *reinterpret_cast<const i32x4*>(wp[rt] + off);
-        wa[u][rt][1] = *reinterpret_cast<const i32x4*>(wp[rt] + off + 16);
+        wa[u][rt][0] = *reinterpret_cast<const i32x4*>(wp[rt] + woff);
+        wa[u][rt][1] = *reinterpret_cast<const i32x4*>(wp[rt] + woff + (PACKW ? 1024 : 16));
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -185,8 +195,12 @@ template <int MT, int RT, int W, int U, bool PACKX, int RANK>
 static void launch_decode(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
                           const DecodePlan& p, float* partial, int* counters, const Epilogue& ep, hipStream_t stream) {
   const dim3 grid((unsigned)p.groups, (unsigned)p.splits), block(64 * W);
-  gemm_decode_kernel<MT, RT, W, U, PACKX, RANK>
-      <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, p.splits, partial, counters, ep);
+  if (ldw == 0)
+    gemm_decode_kernel<MT, RT, W, U, PACKX, RANK, true>
+        <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, p.splits, partial, counters, ep);
+  else
+    gemm_decode_kernel<MT, RT, W, U, PACKX, RANK, false>
+        <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, p.splits, partial, counters, ep);
 }
 
 template <int MT, int RT, bool PACKX, int RANK>

@@ -78,7 +78,15 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int g
   tile_n = r / gsize;
 }
 
-template <int BM, int BN, int WGM, int WGN, int BK, int STAGES, int RANK>
+// Byte offset of stage kt's copy for one 16-byte unit of a tiled weight row,
+// relative to stage 0 (BK-deep stages; tiled_w_offset): a 64-deep stage is
+// half of a 128-deep step fragment, 512 bytes into it for odd kt.
+template <int BK>
+__device__ __forceinline__ int64_t tiled_stage_offset(int kt) {
+  return BK == 128 ? (int64_t)kt * 2048 : (int64_t)(kt >> 1) * 2048 + (kt & 1) * 512;
+}
+
+template <int BM, int BN, int WGM, int WGN, int BK, int STAGES, int RANK, bool PACKW>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint8_t* __restrict__ xq, int64_t ldx,
                                                                       const uint8_t* __restrict__ w, int64_t ldw, int M,
                                                                       int N, int K, int tiles_m, int tiles_n, int group_m,
@@ -114,20 +122,29 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
   // Lane l writes row RPL*g + l/CH at physical chunk l%CH, which holds logical
   // chunk (l%CH) ^ swizzle(row). Rows past M or N re-read the last valid row;
   // their products land in outputs that are never stored.
+  // Tiled weights (PACKW) are gathered from their fragment layout into the
+  // same LDS rows. Each wave-load index i holds only token rows or only
+  // weight rows.
+  static_assert(BM % (NW * RPL) == 0, "wave-loads straddle the token/weight boundary");
   const uint8_t* src[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
     const int r = (i * NW + wave) * RPL + lane / CH;
     const int chunk = (lane % CH) ^ swizzle<BK>(r);
-    src[i] = r < BM ? xq + (int64_t)min(m0 + r, M - 1) * ldx + chunk * 16
-                    : w + (int64_t)min(n0 + r - BM, N - 1) * ldw + chunk * 16;
+    if (r < BM)
+      src[i] = xq + (int64_t)min(m0 + r, M - 1) * ldx + chunk * 16;
+    else if (PACKW)
+      src[i] = w + tiled_w_offset(min(n0 + r - BM, N - 1), chunk * 16, K >> 7);
+    else
+      src[i] = w + (int64_t)min(n0 + r - BM, N - 1) * ldw + chunk * 16;
   }
 
   auto issue_stage = [&](int kt) {
     uint8_t* base = lds + (kt % STAGES) * STAGE;
     const int64_t k0 = (int64_t)kt * BK;
+    const int64_t wk = PACKW ? tiled_stage_offset<BK>(kt) : k0;
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) load_lds16(src[i] + k0, base + (i * NW + wave) * 1024);
+    for (int i = 0; i < LOADS; ++i) load_lds16(src[i] + (i * NW * RPL < BM ? k0 : wk), base + (i * NW + wave) * 1024);
   };
 
   f32x16 acc[TN][TM];
@@ -298,7 +315,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
 // lane half h of the 32x32 operand layout covers k = 32h + [0, 32) of the
 // stage; MFMA q of the stage uses k = 32h + 8q + [0, 8) on both operands.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int WGM, int WGN, int STAGES>
+template <int BM, int BN, int WGM, int WGN, int STAGES, bool PACKW>
 __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_prefill_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw, int M, int N, int K,
     int tiles_m, int tiles_n, int group_m, const float* __restrict__ sw, const uint16_t* __restrict__ bias,
@@ -334,14 +351,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_prefill_kernel(
 #pragma unroll
   for (int i = 0; i < WLOADS; ++i) {
     const int r = (i * NW + wave) * 16 + lane / 4;
-    wsrc[i] = w + (int64_t)min(n0 + r, N - 1) * ldw + ((lane % 4) ^ swizzle<64>(r)) * 16;
+    const int chunk = (lane % 4) ^ swizzle<64>(r);
+    wsrc[i] = PACKW ? w + tiled_w_offset(min(n0 + r, N - 1), chunk * 16, K >> 7)
+                    : w + (int64_t)min(n0 + r, N - 1) * ldw + chunk * 16;
   }
   auto issue_stage = [&](int kt) {
     uint8_t* base = lds + (kt % STAGES) * STAGE;
+    const int64_t wk = PACKW ? tiled_stage_offset<64>(kt) : (int64_t)kt * 64;
 #pragma unroll
     for (int i = 0; i < XLOADS; ++i) load_lds16(xsrc[i] + (int64_t)kt * 128, base + (i * NW + wave) * 1024);
 #pragma unroll
-    for (int i = 0; i < WLOADS; ++i) load_lds16(wsrc[i] + (int64_t)kt * 64, base + XBYTES + (i * NW + wave) * 1024);
+    for (int i = 0; i < WLOADS; ++i) load_lds16(wsrc[i] + wk, base + XBYTES + (i * NW + wave) * 1024);
   };
 
   f32x16 acc[TN][TM];
@@ -448,8 +468,13 @@ static hipError_t launch_w8a16_prefill(const uint16_t* x, int64_t ldx, const uin
                                        const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy, int group_m,
                                        hipStream_t stream) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-  w8a16_prefill_kernel<BM, BN, WGM, WGN, STAGES><<<dim3((unsigned)(tm * tn)), dim3(64 * WGM * WGN), 0, stream>>>(
-      x, ldx, w, ldw, M, N, K, tm, tn, group_m, sw, bias, y, ldy);
+  const dim3 grid((unsigned)(tm * tn)), block(64 * WGM * WGN);
+  if (ldw == 0)
+    w8a16_prefill_kernel<BM, BN, WGM, WGN, STAGES, true><<<grid, block, 0, stream>>>(x, ldx, w, ldw, M, N, K, tm, tn,
+                                                                                     group_m, sw, bias, y, ldy);
+  else
+    w8a16_prefill_kernel<BM, BN, WGM, WGN, STAGES, false><<<grid, block, 0, stream>>>(x, ldx, w, ldw, M, N, K, tm, tn,
+                                                                                      group_m, sw, bias, y, ldy);
   return hipGetLastError();
 }
 
@@ -472,12 +497,17 @@ static hipError_t launch_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* 
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
   const dim3 grid((unsigned)(tm * tn)), block(64 * WGM * WGN);
   if (group_m < 1) group_m = 1;
-  if (rank == 16)
-    gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, 16>
-        <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep);
-  else
-    gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, 0>
-        <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep);
+#define JV_PREFILL_LAUNCH(R, PW)                                   \
+  gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, R, PW>         \
+      <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep)
+  if (rank == 16) {
+    if (ldw == 0) JV_PREFILL_LAUNCH(16, true);
+    else JV_PREFILL_LAUNCH(16, false);
+  } else {
+    if (ldw == 0) JV_PREFILL_LAUNCH(0, true);
+    else JV_PREFILL_LAUNCH(0, false);
+  }
+#undef JV_PREFILL_LAUNCH
   return hipGetLastError();
 }
 
@@ -499,19 +529,23 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
 #define JV_PREFILL_CASE(BM_, BN_, WGM_, WGN_, BK_, ST_)                                                     \
   if (t.bm == BM_ && t.bn == BN_ && t.wgm == WGM_ && t.wgn == WGN_ && t.bk == BK_ && t.stages == ST_)       \
     return launch_prefill<BM_, BN_, WGM_, WGN_, BK_, ST_>(xq, ldx, w, ldw, M, N, K, ep, rank, t.group_m, stream);
+  // The shapes prefill_tile picks.
+  JV_PREFILL_CASE(256, 256, 2, 4, 64, 4)
+  JV_PREFILL_CASE(256, 128, 2, 4, 128, 3)
+  JV_PREFILL_CASE(128, 128, 2, 2, 128, 4)
+#ifdef JV_PREFILL_ALL_TILES
+  // Further shapes for launch-shape sweeps.
   JV_PREFILL_CASE(256, 256, 4, 2, 64, 3)
   JV_PREFILL_CASE(256, 256, 4, 2, 64, 4)
   JV_PREFILL_CASE(256, 256, 2, 4, 64, 3)
-  JV_PREFILL_CASE(256, 256, 2, 4, 64, 4)
-  JV_PREFILL_CASE(256, 128, 2, 4, 128, 3)
   JV_PREFILL_CASE(256, 128, 4, 2, 128, 3)
   JV_PREFILL_CASE(256, 128, 2, 4, 64, 4)
   JV_PREFILL_CASE(256, 128, 4, 2, 64, 4)
   JV_PREFILL_CASE(128, 256, 2, 4, 128, 3)
   JV_PREFILL_CASE(128, 256, 2, 4, 64, 4)
   JV_PREFILL_CASE(128, 128, 2, 2, 128, 3)
-  JV_PREFILL_CASE(128, 128, 2, 2, 128, 4)
   JV_PREFILL_CASE(128, 128, 2, 2, 64, 4)
+#endif
 #undef JV_PREFILL_CASE
   return hipErrorInvalidValue;
 }

@@ -38,6 +38,18 @@ __host__ __device__ inline int64_t packed_x_offset(int m, int k, int ksteps) {
 
 inline int64_t packed_x_bytes(int64_t M, int64_t K) { return (M + 15) / 16 * 16 * K; }
 
+// Tiled weight layout (ldw = 0 for every GEMM launcher here and at the C
+// ABI): the same fragment order for
+// weight codes, row n of the weight being row n of a 16-row tile (the MFMA A
+// side of the decode kernel), so a decode wave's weight load is one
+// contiguous 1 KB per instruction. Needs N % 16 == 0 and K % 128 == 0; the
+// buffer holds N * K bytes.
+__host__ __device__ inline int64_t tiled_w_offset(int n, int k, int ksteps) { return packed_x_offset(n, k, ksteps); }
+
+// Row-major codes <-> tiled layout (16-byte units; in place is not allowed).
+hipError_t tile_weight(const uint8_t* codes, int64_t ldc, int N, int K, uint8_t* tiled, hipStream_t stream);
+hipError_t untile_weight(const uint8_t* tiled, int N, int K, uint8_t* codes, int64_t ldc, hipStream_t stream);
+
 int quant_chunks(int K);
 // packed: write codes in the packed decode layout (codes sized
 // packed_x_bytes(M, K), ldc ignored; the padding rows get zero codes).

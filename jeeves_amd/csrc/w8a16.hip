@@ -27,7 +27,7 @@ __device__ __forceinline__ uint16_t w8a16_out(float acc, float swn, const uint16
 // Weights: lane l holds k bytes [32j, 32j+32) of row l%16 for j = l/16 of each
 // 128-k step; the four 16x16x32 MFMAs q of a step use k = 32j + 8q + [0, 8)
 // on both operands.
-template <int MT, int RT, int W, int U>
+template <int MT, int RT, int W, int U, bool PACKW>
 __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                               const uint8_t* __restrict__ w, int64_t ldw, int M, int N,
                                                               int K, int splits, float* __restrict__ partial,
@@ -46,9 +46,14 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
   const int s_begin = (int)((int64_t)ksteps * slice / slices), s_end = (int)((int64_t)ksteps * (slice + 1) / slices);
 
   const int li = lane & 15, j32 = (lane >> 4) * 32;
+  // Row-major weight rows, or the tiled fragment layout (ldw = 0): the same
+  // 32 bytes per lane and step, as two 16-byte halves 1 KB apart.
   const uint8_t* wp[RT];
+  const int ntiles = (N + 15) >> 4;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) wp[rt] = w + (int64_t)min(n0 + rt * 16 + li, N - 1) * ldw + j32;
+  for (int rt = 0; rt < RT; ++rt)
+    wp[rt] = PACKW ? w + (int64_t)min(group * RT + rt, ntiles - 1) * ksteps * 2048 + lane * 16
+                   : w + (int64_t)min(n0 + rt * 16 + li, N - 1) * ldw + j32;
   const uint16_t* xp[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xp[mt] = x + (int64_t)min(mt * 16 + li, M - 1) * ldx + j32;
@@ -66,10 +71,11 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
     for (int u = 0; u < U; ++u) {
       if (s + u >= s_end) break;
       const int64_t k0 = (int64_t)(s + u) * 128;
+      const int64_t woff = PACKW ? (int64_t)(s + u) * 2048 : k0;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        wa[u][rt][0] = *reinterpret_cast<const i32x4*>(wp[rt] + k0);
-        wa[u][rt][1] = *reinterpret_cast<const i32x4*>(wp[rt] + k0 + 16);
+        wa[u][rt][0] = *reinterpret_cast<const i32x4*>(wp[rt] + woff);
+        wa[u][rt][1] = *reinterpret_cast<const i32x4*>(wp[rt] + woff + (PACKW ? 1024 : 16));
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -151,8 +157,13 @@ static void launch_w8a16_decode(const uint16_t* x, int64_t ldx, const uint8_t* w
                                 const DecodePlan& p, float* partial, int* counters, const float* sw, const uint16_t* bias,
                                 uint16_t* y, int64_t ldy, hipStream_t stream) {
   constexpr int U = w8a16_unroll(MT, RT);
-  w8a16_decode_kernel<MT, RT, W, U><<<dim3((unsigned)p.groups, (unsigned)p.splits), dim3(64 * W), 0, stream>>>(
-      x, ldx, w, ldw, M, N, K, p.splits, partial, counters, sw, bias, y, ldy);
+  const dim3 grid((unsigned)p.groups, (unsigned)p.splits), block(64 * W);
+  if (ldw == 0)
+    w8a16_decode_kernel<MT, RT, W, U, true><<<grid, block, 0, stream>>>(x, ldx, w, ldw, M, N, K, p.splits, partial,
+                                                                          counters, sw, bias, y, ldy);
+  else
+    w8a16_decode_kernel<MT, RT, W, U, false><<<grid, block, 0, stream>>>(x, ldx, w, ldw, M, N, K, p.splits, partial,
+                                                                           counters, sw, bias, y, ldy);
 }
 
 template <int MT>

@@ -80,6 +80,62 @@ def _check_weight(K: int, weight: torch.Tensor) -> None:
                          f"of shape {tuple(weight.shape)}")
 
 
+def _weight_operand(weight: torch.Tensor, tiled: bool) -> tuple[torch.Tensor, int]:
+    """Weight bytes and the C ABI's ldw: the row stride, or 0 for the tiled
+    layout (``tile_weight``)."""
+    w = weight.view(torch.uint8)
+    if tiled:
+        if weight.shape[0] % 16 or not w.is_contiguous():
+            raise ValueError(f"tiled weights are a contiguous [N, K] buffer with N divisible by 16, got {tuple(weight.shape)}")
+        return w, 0
+    if not _rows_aligned(w, 1):
+        w = w.contiguous()
+    return w, w.stride(0)
+
+
+def tileable(out_features: int, in_features: int) -> bool:
+    """Shapes the tiled weight layout covers (whole 16-row tiles, 128-deep steps)."""
+    return out_features % 16 == 0 and in_features % BLOCK_K == 0 and in_features > 0
+
+
+def tile_weight(codes: torch.Tensor) -> torch.Tensor:
+    """Row-major e4m3 codes [N, K] -> the same bytes in the tiled fragment
+    layout (C ABI ``jv_fp8_tile_weight``; ``ldw = 0``), same shape and dtype.
+    For 16-row tile t and 128-deep step s the 2 KB fragment holds two 1 KB
+    halves (h = (k % 32) / 16) of 64 lanes x 16 bytes, lane = n % 16 +
+    16 * ((k % 128) / 32): the order a decode wave loads, 1 KB contiguous per
+    instruction. A layout change only (the reference's Metal path tiles its
+    codes the same way for its kernel, ``inference/fp8_metal.py:23-24``)."""
+    N, K = codes.shape
+    if not tileable(N, K):
+        raise ValueError(f"tiling needs N divisible by 16 and K by {BLOCK_K}, got {N} x {K}")
+    src = codes.view(torch.uint8)
+    if codes.device.type != "cuda":
+        out = src.reshape(N // 16, 16, K // 128, 4, 2, 16).permute(0, 2, 4, 3, 1, 5).contiguous().view(N, K)
+        return out.view(codes.dtype)
+    if not _rows_aligned(src, 1):
+        src = src.contiguous()
+    out = torch.empty(N, K, dtype=torch.uint8, device=codes.device)
+    with torch.cuda.device(codes.device):
+        _lib.check(_lib.lib().jv_fp8_tile_weight(src.data_ptr(), src.stride(0), N, K, out.data_ptr(), _stream(codes.device)))
+    return out.view(codes.dtype)
+
+
+def untile_weight(tiled: torch.Tensor) -> torch.Tensor:
+    """Inverse of ``tile_weight``: row-major codes [N, K]."""
+    N, K = tiled.shape
+    if not tileable(N, K):
+        raise ValueError(f"untiling needs N divisible by 16 and K by {BLOCK_K}, got {N} x {K}")
+    src = tiled.view(torch.uint8).contiguous()
+    if tiled.device.type != "cuda":
+        out = src.view(N // 16, K // 128, 2, 4, 16, 16).permute(0, 4, 1, 3, 2, 5).contiguous().view(N, K)
+        return out.view(tiled.dtype)
+    out = torch.empty(N, K, dtype=torch.uint8, device=tiled.device)
+    with torch.cuda.device(tiled.device):
+        _lib.check(_lib.lib().jv_fp8_untile_weight(src.data_ptr(), N, K, out.data_ptr(), K, _stream(tiled.device)))
+    return out.view(tiled.dtype)
+
+
 def _check_lora(lora, K: int, N: int):
     if lora is None:
         return None, None, 0, 0.0
@@ -92,13 +148,14 @@ def _check_lora(lora, K: int, N: int):
 
 
 def fp8_matmul(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *, bias: torch.Tensor | None = None,
-               lora: tuple[torch.Tensor, torch.Tensor, float] | None = None) -> torch.Tensor:
+               lora: tuple[torch.Tensor, torch.Tensor, float] | None = None, tiled: bool = False) -> torch.Tensor:
     """``y = bf16(quant(x) @ weight^T * scale)`` (``inference/fp8.py:112-148``).
 
     x: bf16 [M,K] with unit column stride (any 16-byte aligned row stride);
     weight: float8_e4m3fn [N,K]; scale: float32 [N]. Returns a new bf16 [M,N]
     on x's device; inputs are never written. ``bias`` (bf16 [N]) and ``lora``
     (``(A [r,K], B [N,r], scaling)``) are folded into the same epilogue.
+    ``tiled``: ``weight`` holds the codes in the ``tile_weight`` layout.
     """
     M, K = x.shape
     N = weight.shape[0]
@@ -109,9 +166,7 @@ def fp8_matmul(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *, bi
         x = x.to(torch.bfloat16)
     if not _rows_aligned(x, 2):
         x = x.contiguous()
-    w = weight.view(torch.uint8)
-    if not _rows_aligned(w, 1):
-        w = w.contiguous()
+    w, ldw = _weight_operand(weight, tiled)
     y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
     if M == 0:
         return y
@@ -125,7 +180,7 @@ def fp8_matmul(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *, bi
         if ws_bytes < 0:
             _lib.check(_lib.JV_ERR_HIP)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-        _lib.check(L.jv_fp8_linear(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), scale.data_ptr(),
+        _lib.check(L.jv_fp8_linear(x.data_ptr(), x.stride(0), w.data_ptr(), ldw, scale.data_ptr(),
                                    bias.data_ptr() if bias is not None else None, a.data_ptr() if rank else None,
                                    b.data_ptr() if rank else None, rank, scaling, y.data_ptr(), N, M, N, K, ws.data_ptr(),
                                    ws_bytes, _lib.counters_ptr(counters), counters.numel() if counters is not None else 0,
@@ -134,7 +189,7 @@ def fp8_matmul(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *, bi
 
 
 def fp8_matmul_w8a16(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *,
-                     bias: torch.Tensor | None = None) -> torch.Tensor:
+                     bias: torch.Tensor | None = None, tiled: bool = False) -> torch.Tensor:
     """W8A16 parity mode: the reference's own arithmetic,
     ``((x.float() @ weight.float().t()) * scale).to(bf16)`` (``model/metal_test.py:213``,
     ``inference/fp8.py:62-99``), then ``+ bias`` in bf16 (``inference/fp8.py:183-184``).
@@ -151,9 +206,7 @@ def fp8_matmul_w8a16(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
         x = x.to(torch.bfloat16)
     if not _rows_aligned(x, 2):
         x = x.contiguous()
-    w = weight.view(torch.uint8)
-    if not _rows_aligned(w, 1):
-        w = w.contiguous()
+    w, ldw = _weight_operand(weight, tiled)
     y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
     if M == 0:
         return y
@@ -167,7 +220,7 @@ def fp8_matmul_w8a16(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
         if ws_bytes < 0:
             _lib.check(_lib.JV_ERR_HIP)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-        _lib.check(L.jv_w8a16_linear(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), scale.data_ptr(),
+        _lib.check(L.jv_w8a16_linear(x.data_ptr(), x.stride(0), w.data_ptr(), ldw, scale.data_ptr(),
                                      bias.data_ptr() if bias is not None else None, y.data_ptr(), N, M, N, K,
                                      ws.data_ptr(), ws_bytes, _lib.counters_ptr(counters),
                                      counters.numel() if counters is not None else 0, _stream(dev)))
@@ -187,12 +240,13 @@ def packed_codes_bytes(rows: int, cols: int) -> int:
 def fp8_matmul_quantized(xq: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *,
                          bias: torch.Tensor | None = None, lora_t: torch.Tensor | None = None,
                          lora_b: torch.Tensor | None = None, lora_scaling: float = 0.0,
-                         packed_rows: int | None = None) -> torch.Tensor:
+                         packed_rows: int | None = None, tiled: bool = False) -> torch.Tensor:
     """The GEMM alone on activations already quantized per token (codes
     float8_e4m3fn/uint8 [M,K] and scales float32 [M]), e.g. by
     ``swiglu_quantize``. ``lora_t`` is ``x A^T`` (float32 [M,r]).
     ``packed_rows=M``: ``xq`` is a flat uint8 buffer of M token rows in the
-    packed fragment order (``swiglu_quantize(..., packed=True)``)."""
+    packed fragment order (``swiglu_quantize(..., packed=True)``). ``tiled``:
+    ``weight`` is in the ``tile_weight`` layout."""
     N = weight.shape[0]
     if packed_rows is not None:
         M, K = packed_rows, weight.shape[1]
@@ -208,9 +262,7 @@ def fp8_matmul_quantized(xq: torch.Tensor, x_scale: torch.Tensor, weight: torch.
     xq = xq.view(torch.uint8)
     if packed_rows is None and not _rows_aligned(xq, 1):
         xq = xq.contiguous()
-    w = weight.view(torch.uint8)
-    if not _rows_aligned(w, 1):
-        w = w.contiguous()
+    w, ldw = _weight_operand(weight, tiled)
     y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
     if M == 0:
         return y
@@ -227,7 +279,7 @@ def fp8_matmul_quantized(xq: torch.Tensor, x_scale: torch.Tensor, weight: torch.
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         _lib.check(L.jv_fp8_gemm(xq.data_ptr(), 0 if packed_rows is not None else xq.stride(0),
                                  x_scale.to(torch.float32).contiguous().data_ptr(), w.data_ptr(),
-                                 w.stride(0), scale.to(torch.float32).contiguous().data_ptr(),
+                                 ldw, scale.to(torch.float32).contiguous().data_ptr(),
                                  bias.data_ptr() if bias is not None else None, lora_t.data_ptr() if rank else None,
                                  lora_b.data_ptr() if rank else None, rank, float(lora_scaling), y.data_ptr(), N, M, N, K,
                                  ws.data_ptr(), ws_bytes, _lib.counters_ptr(counters),
@@ -282,6 +334,13 @@ class FP8Linear(nn.Module):
     and ``scale`` (float32 [N]), optional bf16 ``bias``. ``set_lora`` attaches
     a LoRA adapter (``model/lora.py:122-133``) that the GEMM epilogue adds.
 
+    When the shape allows (``tileable``: N % 16 == 0, K % 128 == 0) the
+    ``weight`` buffer holds the codes in the ``tile_weight`` layout the decode
+    kernels read fastest (``tiled`` is True). The state dict still carries
+    row-major codes under ``weight`` (converted on save and on load), and
+    ``load_codes``/``load_weight`` take row-major codes, so checkpoints and
+    callers see the reference's format; ``codes()`` returns them row-major.
+
     ``activations`` picks the arithmetic: ``"fp8"`` (default) quantizes the
     activations per token and runs the FP8 x FP8 GEMM; ``"bf16"`` is the
     W8A16 parity mode (``fp8_matmul_w8a16``), the reference's own math, for
@@ -296,8 +355,28 @@ class FP8Linear(nn.Module):
         self.register_buffer("scale", torch.empty(out_features, dtype=torch.float32, device=device))
         self.bias = nn.Parameter(torch.empty(out_features, dtype=torch.bfloat16, device=device), requires_grad=False) if bias else None
         self.in_features, self.out_features = in_features, out_features
+        self.tiled = tileable(out_features, in_features)
         self.lora: tuple[torch.Tensor, torch.Tensor, float] | None = None
         self.activations = "fp8"
+        self._register_state_dict_hook(FP8Linear._rowmajor_state)
+        self._register_load_state_dict_pre_hook(FP8Linear._tile_loaded_state, with_module=True)
+
+    @staticmethod
+    def _rowmajor_state(module: "FP8Linear", state: dict, prefix: str, local_metadata) -> None:
+        key = prefix + "weight"
+        if module.tiled and key in state and state[key].device.type != "meta":
+            state[key] = untile_weight(state[key])
+
+    @staticmethod
+    def _tile_loaded_state(module: "FP8Linear", state: dict, prefix: str, local_metadata, strict, missing_keys,
+                           unexpected_keys, error_msgs) -> None:
+        key = prefix + "weight"
+        if module.tiled and key in state and tuple(state[key].shape) == (module.out_features, module.in_features):
+            state[key] = tile_weight(state[key].to(module.weight.device))
+
+    def codes(self) -> torch.Tensor:
+        """The e4m3 codes, row-major [N, K] (a converted copy when tiled)."""
+        return untile_weight(self.weight) if self.tiled else self.weight
 
     def set_activations(self, mode: str) -> None:
         """``"fp8"`` (per-token e4m3 activations) or ``"bf16"`` (W8A16 parity mode)."""
@@ -309,6 +388,9 @@ class FP8Linear(nn.Module):
 
     @torch.no_grad()
     def load_codes(self, codes: torch.Tensor, scale: torch.Tensor) -> None:
+        """Row-major codes [N, K] and their scales (stored tiled when ``tiled``)."""
+        if self.tiled:
+            codes = tile_weight(codes.to(self.weight.device))
         self.weight.copy_(codes)
         self.scale.copy_(scale)
 
@@ -325,11 +407,17 @@ class FP8Linear(nn.Module):
 
     @classmethod
     def concatenated(cls, parts: list["FP8Linear"]) -> "FP8Linear":
+        """One linear over the parts' output rows (``inference/fp8.py:168-175``);
+        the parts become views of its buffers. Tiles are whole 16-row groups,
+        so tiled parts concatenate as they are; if any part is row-major the
+        merged buffer is row-major and every part converts to it."""
         sizes = [p.out_features for p in parts]
         merged = cls(parts[0].in_features, sum(sizes), device="meta")
-        merged.weight, merged.scale = torch.cat([p.weight for p in parts]), torch.cat([p.scale for p in parts])
+        merged.tiled = merged.tiled and all(p.tiled for p in parts)
+        weights = [p.weight if merged.tiled else p.codes() for p in parts]
+        merged.weight, merged.scale = torch.cat(weights), torch.cat([p.scale for p in parts])
         for p, weight, scale in zip(parts, merged.weight.split(sizes), merged.scale.split(sizes)):
-            p.weight, p.scale = weight, scale
+            p.weight, p.scale, p.tiled = weight, scale, merged.tiled
         return merged
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -338,9 +426,9 @@ class FP8Linear(nn.Module):
         if x2.stride(-1) != 1:
             x2 = x2.contiguous()
         if self.activations == "bf16":
-            y = fp8_matmul_w8a16(x2, self.weight, self.scale, bias=self.bias)
+            y = fp8_matmul_w8a16(x2, self.weight, self.scale, bias=self.bias, tiled=self.tiled)
         else:
-            y = fp8_matmul(x2, self.weight, self.scale, bias=self.bias, lora=self.lora)
+            y = fp8_matmul(x2, self.weight, self.scale, bias=self.bias, lora=self.lora, tiled=self.tiled)
         return y.view(*shape[:-1], self.out_features)
 
 
@@ -363,7 +451,7 @@ class FP8SwiGLU(nn.Module):
         if self.down.activations == "bf16":
             # W8A16 parity mode: h = silu(gate) * up in bf16 feeds the down GEMM as is.
             h = swiglu_quantize(gu[:, :inter], gu[:, inter:], return_h=True)[-1]
-            y = fp8_matmul_w8a16(h, self.down.weight, self.down.scale, bias=self.down.bias)
+            y = fp8_matmul_w8a16(h, self.down.weight, self.down.scale, bias=self.down.bias, tiled=self.down.tiled)
             return y.view(*shape[:-1], self.down.out_features)
         lora_a = self.down.lora[0] if self.down.lora is not None else None
         # Decode batches hand the down GEMM its codes in fragment order.
@@ -373,7 +461,7 @@ class FP8SwiGLU(nn.Module):
         y = fp8_matmul_quantized(out[0], out[1], self.down.weight, self.down.scale, bias=self.down.bias, lora_t=lora_t,
                                  lora_b=self.down.lora[1] if lora_a is not None else None,
                                  lora_scaling=self.down.lora[2] if lora_a is not None else 0.0,
-                                 packed_rows=M if packed else None)
+                                 packed_rows=M if packed else None, tiled=self.down.tiled)
         return y.view(*shape[:-1], self.down.out_features)
 
 

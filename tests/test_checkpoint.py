@@ -88,7 +88,7 @@ def test_load_tensors_round_trip(tmp_path):
     assert unexpected == []
     assert loaded == {"q.weight", "q.scale", "o.weight", "o.scale", "o.bias", "head.weight", "norm.weight", "norm.bias"}
     want_codes, want_scale = oracle.quantize_rows(tensors["q.weight"].float().numpy())
-    assert np.array_equal(m.q.weight.view(torch.uint8).numpy(), want_codes)
+    assert np.array_equal(m.q.codes().view(torch.uint8).numpy(), want_codes)
     assert np.array_equal(m.q.scale.numpy(), want_scale)
     assert torch.equal(m.o.bias, tensors["o.bias"]) and torch.equal(m.head.weight, tensors["head.weight"])
 

@@ -33,12 +33,12 @@ def test_load_weight_equals_quantize_rows_and_load_codes():
     m = FP8Linear(4096, 1040, device="cuda")
     m.load_weight(w)
     codes, scale = quantize_rows(w)
-    assert torch.equal(m.weight.view(torch.uint8), codes.view(torch.uint8)) and torch.equal(m.scale, scale)
+    assert torch.equal(m.codes().view(torch.uint8), codes.view(torch.uint8)) and torch.equal(m.scale, scale)
     n = FP8Linear(4096, 1040, device="cuda")
     n.load_codes(codes, scale)
     assert torch.equal(n.weight.view(torch.uint8), m.weight.view(torch.uint8)) and torch.equal(n.scale, m.scale)
     want_c, want_s = oracle.quantize_rows(w.float().cpu().numpy())
-    assert np.array_equal(helpers.codes_np(m.weight), want_c)
+    assert np.array_equal(helpers.codes_np(m.codes()), want_c)
 
 
 def test_forward_shapes_bias_and_dtype():
@@ -49,7 +49,7 @@ def test_forward_shapes_bias_and_dtype():
     y = m(x)
     assert y.shape == (3, 16, 1024) and y.dtype == torch.bfloat16
     x2 = x.reshape(-1, 4096).to(torch.bfloat16)
-    nobias = fp8_matmul(x2, m.weight, m.scale)
+    nobias = fp8_matmul(x2, m.weight, m.scale, tiled=m.tiled)
     # fused bias: equals the exact sum rounded once, within one bf16 step of nobias + bias
     ref = (nobias.float() + lin.bias.float()).to(torch.bfloat16)
     assert torch.allclose(y.reshape(-1, 1024).float(), ref.float(), rtol=2 ** -7, atol=1e-2)
@@ -113,7 +113,7 @@ def test_decoder_layer_stack_with_lora():
         bf = oracle.bf16_to_f32(helpers.bits(b)).astype(np.float64)
         if name != "down":
             y = m(x)
-            exact = oracle.gemm_exact_f64(xq, sx, helpers.codes_np(m.weight), m.scale.cpu().numpy()) + \
+            exact = oracle.gemm_exact_f64(xq, sx, helpers.codes_np(m.codes()), m.scale.cpu().numpy()) + \
                 oracle.lora_f64(xf, af, bf, synthetic.LORA_SCALING)
         else:
             inter = synthetic.INTERMEDIATE
@@ -121,11 +121,11 @@ def test_decoder_layer_stack_with_lora():
             codes, scales, t, h = swiglu_quantize(gu[:, :inter], gu[:, inter:], lora_a=m.lora[0], return_h=True)
             from jeeves_amd.fp8 import fp8_matmul_quantized
             y = fp8_matmul_quantized(codes, scales, m.weight, m.scale, lora_t=t, lora_b=m.lora[1],
-                                     lora_scaling=m.lora[2])
+                                     lora_scaling=m.lora[2], tiled=m.tiled)
             hq, hs = oracle.quantize_rows(h.float().cpu().numpy())
             assert np.array_equal(hq, helpers.codes_np(codes))
             hf = oracle.bf16_to_f32(helpers.bits(h)).astype(np.float64)
-            exact = oracle.gemm_exact_f64(hq, hs, helpers.codes_np(m.weight), m.scale.cpu().numpy()) + \
+            exact = oracle.gemm_exact_f64(hq, hs, helpers.codes_np(m.codes()), m.scale.cpu().numpy()) + \
                 oracle.lora_f64(hf, af, bf, synthetic.LORA_SCALING)
         outs[name] = y
         got = oracle.bf16_to_f32(helpers.bits(y)).astype(np.float64)

@@ -141,7 +141,7 @@ def test_w8a16_module_mode():
     lin.bias.copy_((torch.randn(N, generator=g) * 0.1).to(torch.bfloat16))
     lin.set_activations("bf16")
     x = torch.randn(3, 5, K, generator=g).to(torch.bfloat16).cuda()
-    assert torch.equal(lin(x), (fp8_matmul_w8a16(x.reshape(-1, K), lin.weight, lin.scale) + lin.bias).view(3, 5, N))
+    assert torch.equal(lin(x), (fp8_matmul_w8a16(x.reshape(-1, K), lin.weight, lin.scale, tiled=lin.tiled) + lin.bias).view(3, 5, N))
     with pytest.raises(ValueError):
         lin.set_lora(torch.zeros(16, K), torch.zeros(N, 16), 1.0)
 
@@ -155,9 +155,9 @@ def test_w8a16_module_mode():
     block = FP8SwiGLU(gate_up, down)
     for M in (4, 100):
         xm = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
-        gu = fp8_matmul_w8a16(xm, gate_up.weight, gate_up.scale)
+        gu = fp8_matmul_w8a16(xm, gate_up.weight, gate_up.scale, tiled=gate_up.tiled)
         h = oracle.swiglu_bf16(helpers.bits(gu[:, :inter]), helpers.bits(gu[:, inter:]))
-        want = fp8_matmul_w8a16(helpers.from_bits(h, "cuda"), down.weight, down.scale)
+        want = fp8_matmul_w8a16(helpers.from_bits(h, "cuda"), down.weight, down.scale, tiled=down.tiled)
         assert torch.equal(block(xm), want)
 
 

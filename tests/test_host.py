@@ -61,6 +61,35 @@ def test_concatenated_parts_become_views():
         assert p.scale.untyped_storage().data_ptr() == merged.scale.untyped_storage().data_ptr()
 
 
+def test_tiled_layout_on_host():
+    """tile_weight's byte order is the C ABI's (fragment of 16 rows x 128 k:
+    two 1 KB halves of 64 lanes x 16 bytes, lane = n%16 + 16*((k%128)/32)),
+    untile_weight inverts it, and FP8Linear keeps row-major codes in its state
+    dict while storing them tiled."""
+    from jeeves_amd.fp8 import tile_weight, tileable, untile_weight
+
+    g = torch.Generator().manual_seed(3)
+    N, K = 48, 384
+    codes = torch.randint(0, 256, (N, K), generator=g, dtype=torch.uint8)
+    tiled = tile_weight(codes).view(-1)
+    for n, k in ((0, 0), (5, 17), (31, 127), (37, 300), (47, 383)):
+        kk = k % 128
+        off = ((n // 16 * (K // 128) + k // 128) * 2 + (kk // 16) % 2) * 1024 + (n % 16 + 16 * (kk // 32)) * 16 + k % 16
+        assert tiled[off] == codes[n, k]
+    assert torch.equal(untile_weight(tiled.view(N, K)), codes)
+    assert tileable(1024, 4096) and not tileable(1000, 4096) and not tileable(1024, 4000)
+    m = FP8Linear(K, N)
+    assert m.tiled
+    m.load_codes(codes.view(FP8), torch.ones(N))
+    assert torch.equal(m.weight.view(torch.uint8).view(-1), tiled)
+    assert torch.equal(m.state_dict()["weight"].view(torch.uint8), codes)
+    assert torch.equal(m.codes().view(torch.uint8), codes)
+    other = FP8Linear(K, N)
+    other.load_state_dict(m.state_dict())
+    assert torch.equal(other.weight.view(torch.uint8), m.weight.view(torch.uint8))
+    assert not FP8Linear(K, 1000, device="meta").tiled
+
+
 def test_fp8_matmul_validates_before_launch():
     x = torch.zeros(4, 100, dtype=torch.bfloat16)
     w = torch.zeros(64, 100, dtype=torch.uint8).view(FP8)
