@@ -122,21 +122,33 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
   // Lane l writes row RPL*g + l/CH at physical chunk l%CH, which holds logical
   // chunk (l%CH) ^ swizzle(row). Rows past M or N re-read the last valid row;
   // their products land in outputs that are never stored.
-  // Tiled weights (PACKW) are gathered from their fragment layout into the
-  // same LDS rows. Each wave-load index i holds only token rows or only
-  // weight rows.
+  // Tiled weights (PACKW) keep their fragment order in LDS too: the weight
+  // part of a stage is, per 16-row tile, the stage's share of the tile's
+  // 128-deep step fragment -- both 1 KB halves for 128-deep stages, or the
+  // 512-byte piece of each half that a 64-deep stage covers -- so each weight
+  // wave-load copies contiguous global memory (one 1 KB half, or two 512-byte
+  // pieces) into its contiguous 1 KB of LDS. Each wave-load index i holds
+  // only token rows or only weight data.
   static_assert(BM % (NW * RPL) == 0, "wave-loads straddle the token/weight boundary");
+  const int ntiles = (N + 15) >> 4;
   const uint8_t* src[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
-    const int r = (i * NW + wave) * RPL + lane / CH;
+    const int g = i * NW + wave;
+    const int r = g * RPL + lane / CH;
     const int chunk = (lane % CH) ^ swizzle<BK>(r);
-    if (r < BM)
+    if (r < BM) {
       src[i] = xq + (int64_t)min(m0 + r, M - 1) * ldx + chunk * 16;
-    else if (PACKW)
-      src[i] = w + tiled_w_offset(min(n0 + r - BM, N - 1), chunk * 16, K >> 7);
-    else
+    } else if (PACKW) {
+      const int gw = g - BM / RPL;  // weight wave-load: tile gw (64-deep) or half gw%2 of tile gw/2
+      const int tt = BK == 128 ? gw >> 1 : gw;
+      const int h = BK == 128 ? gw & 1 : lane >> 5;
+      const int lp = BK == 128 ? lane : lane & 31;
+      const int tile = min((n0 >> 4) + tt, ntiles - 1);
+      src[i] = w + (((int64_t)tile * (K >> 7)) * 2 + h) * 1024 + lp * 16;
+    } else {
       src[i] = w + (int64_t)min(n0 + r - BM, N - 1) * ldw + chunk * 16;
+    }
   }
 
   auto issue_stage = [&](int kt) {
@@ -180,13 +192,30 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
   // Two fragment sets: while the MFMAs of 64-deep step u run on one set, the
   // LDS reads of step u+1 fill the other.
   i32x8 fa[2][TN], fb[2][TM];
+  // Tiled weights in LDS: row rr of the tile's channels, 64-deep step s of
+  // the stage, k half kh = l/32: lane rr%16 + 16*(2s + kh) of the fragment
+  // (128-deep stages: halves 1 KB apart, 2 KB per tile) or lane
+  // rr%16 + 16*kh of the stage's piece (64-deep: halves 512 bytes apart, 1 KB
+  // per tile). A 16-lane phase reads 256 consecutive bytes.
+  constexpr int TSTRIDE = BK == 128 ? 2048 : 1024, HSTRIDE = BK == 128 ? 1024 : 512;
+  int aoff[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int rr = wn * WN + j * 32 + frow;
+    aoff[j] = BM * BK + (rr >> 4) * TSTRIDE + ((rr & 15) + 16 * (lane >> 5)) * 16;
+  }
   auto load_frags = [&](int kt, int s, i32x8 (&a)[TN], i32x8 (&b)[TM]) {
     const uint8_t* base = lds + (kt % STAGES) * STAGE;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int r = arow[j], sw = swizzle<BK>(r);
-      a[j] = cat8(lds_read16(base + r * BK + ((4 * s + fhalf) ^ sw) * 16),
-                  lds_read16(base + r * BK + ((4 * s + fhalf + 1) ^ sw) * 16));
+      if constexpr (PACKW) {
+        const uint8_t* p = base + aoff[j] + s * 512;
+        a[j] = cat8(lds_read16(p), lds_read16(p + HSTRIDE));
+      } else {
+        const int r = arow[j], sw = swizzle<BK>(r);
+        a[j] = cat8(lds_read16(base + r * BK + ((4 * s + fhalf) ^ sw) * 16),
+                    lds_read16(base + r * BK + ((4 * s + fhalf + 1) ^ sw) * 16));
+      }
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
