@@ -66,6 +66,25 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   for (int mt = 0; mt < MT; ++mt)
     xp[mt] = PACKX ? xq + (int64_t)mt * ksteps * 2048 + lane * 16 : xq + (int64_t)min(mt * 16 + li, M - 1) * ldxq + lk;
 
+  // Each thread's outputs (idx = threadIdx.x + j * 64 WAVES; channel fastest)
+  // and their scales and bias, loaded before the weight stream so the
+  // epilogue does not wait for another memory round trip. Indices are clamped
+  // so the loads are unconditional; a missing bias reads the scales instead.
+  constexpr int kOut = RT * MT * 256, kThreads = 64 * WAVES, kPer = (kOut + kThreads - 1) / kThreads;
+  float pre_sx[kPer], pre_sw[kPer], pre_b[kPer];
+  {
+    const uint16_t* bsrc = ep.bias ? ep.bias : reinterpret_cast<const uint16_t*>(ep.sw);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int idx = min((int)threadIdx.x + j * kThreads, kOut - 1);
+      const int t = idx >> 8, e = idx & 255;
+      const int m = min((t % MT) * 16 + (e >> 4), M - 1), n = min(n0 + (t / MT) * 16 + (e & 15), N - 1);
+      pre_sx[j] = ep.sx[m];
+      pre_sw[j] = ep.sw[n];
+      pre_b[j] = bf16_to_f32(bsrc[n]);
+    }
+  }
+
   f32x4 acc[RT][MT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
@@ -123,8 +142,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   // with rows = weight channels and cols = tokens). Threads walk n fastest so
   // consecutive threads store consecutive channels of one token.
   const float* redf = reinterpret_cast<const float*>(&red[0][0][0]);
-  constexpr int kOut = RT * MT * 256;
-  for (int idx = threadIdx.x; idx < kOut; idx += 64 * WAVES) {
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int idx = (int)threadIdx.x + j * kThreads;
+    if (kOut % kThreads != 0 && idx >= kOut) break;
     const int t = idx >> 8, rt = t / MT, mt = t % MT, e = idx & 255, ml = e >> 4, nl = e & 15;
     const int src = (t * 64 + ml + 16 * (nl >> 2)) * 4 + (nl & 3);
     float sum = 0.0f;
@@ -133,7 +154,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
     const int m = mt * 16 + ml, n = n0 + rt * 16 + nl;
     if (m < M && n < N) {
       if (splits == 1)
-        ep.y[(int64_t)m * ep.ldy + n] = (uint16_t)f32_to_bf16(epilogue_value<RANK>(ep, sum, m, n, ep.sx[m], ep.sw[n]));
+        ep.y[(int64_t)m * ep.ldy + n] =
+            (uint16_t)f32_to_bf16(epilogue_value<RANK>(ep, sum, m, n, pre_sx[j], pre_sw[j], pre_b[j]));
       else  // device-coherent store: visible to the reducing workgroup without a cache flush
         __hip_atomic_store(partial + ((int64_t)split * M + m) * N + n, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -149,14 +171,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
     is_last = __hip_atomic_fetch_add(counters + group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
   __syncthreads();
   if (!is_last) return;
-  for (int idx = threadIdx.x; idx < kOut; idx += 64 * WAVES) {
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int idx = (int)threadIdx.x + j * kThreads;
+    if (kOut % kThreads != 0 && idx >= kOut) break;
     const int t = idx >> 8, rt = t / MT, mt = t % MT, e = idx & 255, ml = e >> 4, nl = e & 15;
     const int m = mt * 16 + ml, n = n0 + rt * 16 + nl;
     if (m < M && n < N) {
       float sum = 0.0f;
       for (int sp = 0; sp < splits; ++sp)
         sum += __hip_atomic_load(partial + ((int64_t)sp * M + m) * N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ep.y[(int64_t)m * ep.ldy + n] = (uint16_t)f32_to_bf16(epilogue_value<RANK>(ep, sum, m, n, ep.sx[m], ep.sw[n]));
+      ep.y[(int64_t)m * ep.ldy + n] =
+          (uint16_t)f32_to_bf16(epilogue_value<RANK>(ep, sum, m, n, pre_sx[j], pre_sw[j], pre_b[j]));
     }
   }
   if (threadIdx.x == 0) __hip_atomic_store(counters + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
