@@ -18,9 +18,10 @@ namespace jv {
 
 // y = bf16(acc * sw), then bf16(y + bias) when there is a bias: the two
 // roundings of the reference's GEMM output and its separate bias add.
-__device__ __forceinline__ uint16_t w8a16_out(float acc, float swn, const uint16_t* bias, int n) {
+// biasn is the bias of the channel, already loaded (read only when has_bias).
+__device__ __forceinline__ uint16_t w8a16_out(float acc, float swn, bool has_bias, float biasn) {
   uint32_t v = f32_to_bf16(acc * swn);
-  if (bias) v = f32_to_bf16(bf16_to_f32(v) + bf16_to_f32(bias[n]));
+  if (has_bias) v = f32_to_bf16(bf16_to_f32(v) + biasn);
   return (uint16_t)v;
 }
 
@@ -57,6 +58,24 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
   const uint16_t* xp[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xp[mt] = x + (int64_t)min(mt * 16 + li, M - 1) * ldx + j32;
+
+  // Each thread's output channels (idx = threadIdx.x + j * 64 W; channel
+  // fastest) and their scales and bias, loaded before the weight stream so the
+  // epilogue does not wait for another memory round trip; clamped indices keep
+  // the loads unconditional, and a missing bias reads the scales instead.
+  constexpr int kOut = RT * MT * 256, kThreads = 64 * W, kPer = (kOut + kThreads - 1) / kThreads;
+  float pre_sw[kPer], pre_b[kPer];
+  {
+    const uint16_t* bsrc = bias ? bias : reinterpret_cast<const uint16_t*>(sw);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int idx = min((int)threadIdx.x + j * kThreads, kOut - 1);
+      const int n = min(n0 + ((idx >> 8) / MT) * 16 + (idx & 15), N - 1);
+      pre_sw[j] = sw[n];
+      pre_b[j] = bf16_to_f32(bsrc[n]);
+    }
+  }
+  const bool has_bias = bias != nullptr;
 
   f32x4 acc[RT][MT];
 #pragma unroll
@@ -109,8 +128,10 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
   // Output (token ml, channel nl) of tile (rt, mt) sits in lane ml + 16*(nl/4),
   // register nl % 4 (16x16 layout: row = 4*(lane/16) + reg is the channel).
   const float* redf = reinterpret_cast<const float*>(&red[0][0][0]);
-  constexpr int kOut = RT * MT * 256;
-  for (int idx = threadIdx.x; idx < kOut; idx += 64 * W) {
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int idx = (int)threadIdx.x + j * kThreads;
+    if (kOut % kThreads != 0 && idx >= kOut) break;
     const int t = idx >> 8, rt = t / MT, mt = t % MT, e = idx & 255, ml = e >> 4, nl = e & 15;
     const int src = (t * 64 + ml + 16 * (nl >> 2)) * 4 + (nl & 3);
     float sum = 0.0f;
@@ -119,7 +140,7 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
     const int m = mt * 16 + ml, n = n0 + rt * 16 + nl;
     if (m < M && n < N) {
       if (splits == 1)
-        y[(int64_t)m * ldy + n] = w8a16_out(sum, sw[n], bias, n);
+        y[(int64_t)m * ldy + n] = w8a16_out(sum, pre_sw[j], has_bias, pre_b[j]);
       else  // device-coherent store: visible to the reducing workgroup without a cache flush
         __hip_atomic_store(partial + ((int64_t)split * M + m) * N + n, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -135,14 +156,17 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
     is_last = __hip_atomic_fetch_add(counters + group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
   __syncthreads();
   if (!is_last) return;
-  for (int idx = threadIdx.x; idx < kOut; idx += 64 * W) {
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int idx = (int)threadIdx.x + j * kThreads;
+    if (kOut % kThreads != 0 && idx >= kOut) break;
     const int t = idx >> 8, rt = t / MT, mt = t % MT, e = idx & 255, ml = e >> 4, nl = e & 15;
     const int m = mt * 16 + ml, n = n0 + rt * 16 + nl;
     if (m < M && n < N) {
       float sum = 0.0f;
       for (int sp = 0; sp < splits; ++sp)
         sum += __hip_atomic_load(partial + ((int64_t)sp * M + m) * N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      y[(int64_t)m * ldy + n] = w8a16_out(sum, sw[n], bias, n);
+      y[(int64_t)m * ldy + n] = w8a16_out(sum, pre_sw[j], has_bias, pre_b[j]);
     }
   }
   if (threadIdx.x == 0) __hip_atomic_store(counters + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
