@@ -119,21 +119,16 @@ def build_set(torch, synthetic, quantize_rows, M: int, case):
 
 
 def quantized_operands(torch, fp8, x):
-    """Activation codes as fp8_matmul hands them to its GEMM: packed fragment
-    order for decode batches, row-major above."""
+    """Activation codes as fp8_matmul hands them to its GEMM: the packed
+    fragment order (rows of up to 16384 channels, as in every workload here)."""
     from jeeves_amd import _lib
 
     M, K = x.shape
     sx = torch.empty(M, dtype=torch.float32, device=x.device)
-    if M <= fp8.DECODE_MAX_ROWS:
-        codes = torch.empty(fp8.packed_codes_bytes(M, K), dtype=torch.uint8, device=x.device)
-        _lib.check(_lib.lib().jv_fp8_quantize_rows_bf16(x.data_ptr(), x.stride(0), M, K, codes.data_ptr(), 0, sx.data_ptr(),
-                                                        torch.cuda.current_stream().cuda_stream))
-        return codes, sx, M
-    codes = torch.empty(M, K, dtype=torch.uint8, device=x.device)
-    _lib.check(_lib.lib().jv_fp8_quantize_rows_bf16(x.data_ptr(), x.stride(0), M, K, codes.data_ptr(), K, sx.data_ptr(),
+    codes = torch.empty(fp8.packed_codes_bytes(M, K), dtype=torch.uint8, device=x.device)
+    _lib.check(_lib.lib().jv_fp8_quantize_rows_bf16(x.data_ptr(), x.stride(0), M, K, codes.data_ptr(), 0, sx.data_ptr(),
                                                     torch.cuda.current_stream().cuda_stream))
-    return codes, sx, None
+    return codes, sx, M
 
 
 def kernel_ms(b: Bench, fp8, rot, operands, name: str, replays: int) -> float:
@@ -311,7 +306,7 @@ def main() -> int:
         pk_tf = 2 * Mp * N * K / (pk * 1e-3) / 1e12
         result["prefill"] = {
             "tokens": Mp, "ms_per_step": round(pms, 4), "TFLOP/s": round(flops / (pms * 1e-3) / 1e12, 1),
-            "roofline": {"bound": "mfma", "kernel": "gemm_prefill_kernel (gate+up, N=24576 K=4096, M=2048)",
+            "roofline": {"bound": "mfma", "kernel": "gemm_prefill_pp_kernel (gate+up, N=24576 K=4096, M=2048)",
                          "achieved": round(pk_tf, 1), "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(pk_tf / FP8_PEAK_TFLOPS, 4), "avg_launch_us": round(pk * 1e3, 2),
                          "traffic": measured_traffic(f"prefill_gate_up_m{Mp}"),

@@ -53,10 +53,12 @@ int jv_device_cu_count(int device);
  *   codes[r,c] = e4m3fn(x[r,c] / scales[r])   (IEEE quotient, RNE, NaN on overflow)
  * x: [rows, cols] bf16, row stride ldx; codes: [rows, cols] bytes, row stride
  * ldc; scales: [rows] fp32. cols must be a positive multiple of 8.
- * ldc = 0 writes the codes in the decode GEMM's packed fragment order instead
- * (rows <= JV_FP8_DECODE_MAX_ROWS, cols a multiple of 128 up to 16384; the
- * buffer holds jv_fp8_packed_codes_bytes(rows, cols) bytes), for jv_fp8_gemm
- * with ldxq = 0.
+ * ldc = 0 writes the codes in the GEMMs' packed fragment order instead (the
+ * tiled weight layout below applied to token rows, rows padded to a multiple
+ * of 16 with zero codes; cols a multiple of 128 up to 16384; the buffer holds
+ * jv_fp8_packed_codes_bytes(rows, cols) bytes), for jv_fp8_gemm with
+ * ldxq = 0. Both the decode and the prefill GEMMs read that order fastest, and
+ * jv_fp8_linear uses it for its own codes.
  * Used for per-token activation quantization and for FP8Linear.load_weight
  * (inference/fp8.py:164-166). */
 int jv_fp8_quantize_rows_bf16(const void* x, int64_t ldx, int64_t rows, int64_t cols, void* codes, int64_t ldc,
@@ -120,7 +122,7 @@ int64_t jv_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 /* The GEMM and epilogue alone on already-quantized activations
  * (_fp8_matmul, inference/fp8.py:62-99, with FP8 x FP8 operands):
  * xq: [M,K] e4m3fn (row stride ldxq; ldxq = 0: the packed fragment order of
- * jv_fp8_quantize_rows_bf16 with ldc = 0, M <= JV_FP8_DECODE_MAX_ROWS);
+ * jv_fp8_quantize_rows_bf16 with ldc = 0);
  * x_scale: [M] fp32; lora_t: [M,rank] fp32 low-rank activations or NULL;
  * other arguments as jv_fp8_linear. */
 int jv_fp8_gemm(const void* xq, int64_t ldxq, const float* x_scale, const void* w, int64_t ldw, const float* w_scale,

@@ -60,10 +60,10 @@ int64_t partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
   return s > 1 ? round_up((int64_t)s * M * N * 4, 256) : 0;
 }
 
-// Activation codes for jv_fp8_linear: packed decode layout for M <= 64, row-major above.
-int64_t codes_bytes(int64_t M, int64_t K) {
-  return M <= jv::kDecodeMaxRows ? jv::packed_x_bytes(M, K) : M * K;
-}
+// Activation codes for jv_fp8_linear: the packed fragment order whenever the
+// single-pass quantizer covers the row (K <= 16384), row-major above.
+bool packed_codes(int64_t K) { return jv::quant_chunks((int)K) != 0; }
+int64_t codes_bytes(int64_t M, int64_t K) { return packed_codes(K) ? jv::packed_x_bytes(M, K) : M * K; }
 
 int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, const uint8_t* w, int64_t ldw, const float* sw,
              const uint16_t* bias, const float* lora_t, const uint16_t* lora_b, int64_t rank, float lora_scaling, uint16_t* y,
@@ -71,7 +71,8 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, co
              int32_t* counters, int64_t n_counters, hipStream_t stream) {
   const int cus = cu_count_of(-1);
   if (cus <= 0) return fail(JV_ERR_HIP, "cannot query the device's compute units");
-  if ((uint64_t)M * (uint64_t)ldxq >= (1ull << 32)) return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
+  if ((uint64_t)M * (uint64_t)ldxq >= (1ull << 32) || (uint64_t)jv::packed_x_bytes(M, K) >= (1ull << 32))
+    return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
   jv::Epilogue ep{sx, sw, bias, lora_t, lora_b, lora_scaling, y, ldy};
   if (M <= jv::kDecodeMaxRows) {
     const jv::DecodePlan plan = jv::decode_plan(M, N, K, cus);
@@ -92,7 +93,7 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, co
                       "fp8 decode GEMM launch");
   }
   const jv::PrefillTile tile = jv::prefill_tile(M, N, cus);
-  return hip_status(jv::gemm_prefill(xq, ldxq, w, ldw, (int)M, (int)N, (int)K, ep, (int)rank, tile, stream),
+  return hip_status(jv::gemm_prefill(xq, packed_x ? 0 : ldxq, w, ldw, (int)M, (int)N, (int)K, ep, (int)rank, tile, stream),
                     "fp8 prefill GEMM launch");
 }
 
@@ -131,9 +132,8 @@ int jv_fp8_quantize_rows_bf16(const void* x, int64_t ldx, int64_t rows, int64_t 
     return fail(JV_ERR_VALUE, "quantize_rows needs a positive column count divisible by 8, got %lld", (long long)cols);
   if (rows == 0) return JV_OK;
   const bool packed = ldc == 0;
-  if (packed && (rows > jv::kDecodeMaxRows || cols % JV_FP8_BLOCK_K || jv::quant_chunks((int)cols) == 0))
-    return fail(JV_ERR_VALUE, "the packed layout needs at most %d rows and a column count divisible by %d up to 16384",
-                jv::kDecodeMaxRows, JV_FP8_BLOCK_K);
+  if (packed && (cols % JV_FP8_BLOCK_K || jv::quant_chunks((int)cols) == 0))
+    return fail(JV_ERR_VALUE, "the packed layout needs a column count divisible by %d up to 16384", JV_FP8_BLOCK_K);
   if (!aligned16(x) || (ldx * 2) % 16 || !aligned16(codes) || ldc % 16)
     return fail(JV_ERR_VALUE, "quantize_rows needs 16-byte aligned rows");
   return hip_status(jv::quant_rows_bf16((const uint16_t*)x, ldx, rows, (int)cols, (uint8_t*)codes, ldc, scales, nullptr, 0,
@@ -142,7 +142,7 @@ int jv_fp8_quantize_rows_bf16(const void* x, int64_t ldx, int64_t rows, int64_t 
 }
 
 int64_t jv_fp8_packed_codes_bytes(int64_t rows, int64_t cols) {
-  if (rows < 0 || rows > jv::kDecodeMaxRows || cols <= 0 || cols % JV_FP8_BLOCK_K) return -1;
+  if (rows < 0 || rows > INT32_MAX || cols <= 0 || cols > INT32_MAX || cols % JV_FP8_BLOCK_K) return -1;
   return jv::packed_x_bytes(rows, cols);
 }
 
@@ -177,8 +177,6 @@ int jv_fp8_gemm(const void* xq, int64_t ldxq, const float* x_scale, const void* 
   if (int rc = check_lora(lora_rank, lora_t, lora_b)) return rc;
   if (M == 0) return JV_OK;
   const bool packed = ldxq == 0;
-  if (packed && M > jv::kDecodeMaxRows)
-    return fail(JV_ERR_VALUE, "packed activation codes hold at most %d rows, got %lld", jv::kDecodeMaxRows, (long long)M);
   if (!aligned16(xq) || ldxq % 16) return fail(JV_ERR_VALUE, "the fp8 GEMM needs 16-byte aligned operand rows");
   if (int rc = check_weight(N, K, ldw, w)) return rc;
   return run_gemm((const uint8_t*)xq, ldxq, packed, x_scale, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t,
@@ -203,7 +201,7 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
     return fail(JV_ERR_VALUE, "workspace needs %lld bytes, 256-byte aligned", (long long)need);
   uint8_t* ws = (uint8_t*)workspace;
   uint8_t* codes = ws;
-  const bool packed = M <= jv::kDecodeMaxRows;
+  const bool packed = packed_codes(K);
   ws += round_up(codes_bytes(M, K), 256);
   float* sx = (float*)ws;
   ws += round_up(M * 4, 256);
@@ -215,7 +213,7 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
                                               (int)lora_rank, lora_t, packed, s),
                           "activation quantization launch"))
     return rc;
-  return run_gemm(codes, K, packed, sx, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t, (const uint16_t*)lora_b,
+  return run_gemm(codes, packed ? 0 : K, packed, sx, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t, (const uint16_t*)lora_b,
                   lora_rank, lora_scaling, (uint16_t*)y, ldy, M, N, K, ws, rest, tile_counters, n_counters, s);
 }
 
@@ -260,9 +258,8 @@ int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_
   if (int rc = check_lora(lora_rank, lora_a, lora_t)) return rc;
   if (M == 0) return JV_OK;
   const bool packed = ldc == 0;
-  if (packed && (M > jv::kDecodeMaxRows || I % JV_FP8_BLOCK_K))
-    return fail(JV_ERR_VALUE, "the packed layout needs at most %d rows and I divisible by %d", jv::kDecodeMaxRows,
-                JV_FP8_BLOCK_K);
+  if (packed && I % JV_FP8_BLOCK_K)
+    return fail(JV_ERR_VALUE, "the packed layout needs I divisible by %d", JV_FP8_BLOCK_K);
   if (!aligned16(gate) || (ldg * 2) % 16 || !aligned16(up) || (ldu * 2) % 16 || !aligned16(codes) || ldc % 16 ||
       (h_out && (!aligned16(h_out) || (ldh * 2) % 16)))
     return fail(JV_ERR_VALUE, "swiglu_quantize needs 16-byte aligned rows");

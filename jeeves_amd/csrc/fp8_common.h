@@ -32,6 +32,15 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
 }
 
+// Two floats -> two bf16 (a in the low half), round to nearest even, with
+// gfx950's v_cvt_pk_bf16_f32. Equal to f32_to_bf16 on every non-NaN input; a
+// NaN stays a NaN (its sign and payload are not canonicalised to 0x7FC0).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
+}
+
 // ---------------------------------------------------------------------------
 // e4m3fn encode, round to nearest even, NaN on overflow (|f| > 464), sign kept.
 // Written from the OCP FP8 v1.0 format definition; this is the semantics of

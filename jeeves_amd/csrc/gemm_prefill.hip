@@ -86,7 +86,71 @@ __device__ __forceinline__ int64_t tiled_stage_offset(int kt) {
   return BK == 128 ? (int64_t)kt * 2048 : (int64_t)(kt >> 1) * 2048 + (kt & 1) * 512;
 }
 
-template <int BM, int BN, int WGM, int WGN, int BK, int STAGES, int RANK, bool PACKW>
+// Epilogue of both FP8 prefill kernels. 32x32 MFMA output layout: lane l
+// holds column l % 32 (a token) and, in register r, row 8*(r/4) + 4*(l/32) +
+// r%4 (a channel): each register quad is 4 consecutive channels of one token.
+// The finished bf16 tile goes through LDS ([BM tokens][BN channels], 16-byte
+// chunk c of row r stored at chunk c ^ (r % OUT_CH)) so that global stores are
+// 16 bytes per lane over whole row segments. The caller's operand reads and
+// copies into `lds` are complete (this wave's) when it is called.
+template <int BM, int BN, int WGM, int WGN, int RANK>
+__device__ __forceinline__ void store_tile(uint8_t* lds, const float* scale_lds,
+                                           const f32x16 (&acc)[BN / WGN / 32][BM / WGM / 32], const Epilogue& ep, int m0,
+                                           int n0, int M, int N, int wm, int wn, int lane) {
+  constexpr int NW = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int OUT_CH = BN * 2 / 16;  // 16-byte chunks per output tile row
+  static_assert(OUT_CH <= 32 && (OUT_CH & (OUT_CH - 1)) == 0, "output tile width");
+  float sxm[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) sxm[i] = scale_lds[wm * WM + i * 32 + (lane & 31)];
+  // Every wave's operand reads are complete before the tile overwrites them.
+  lds_barrier();
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int nl = wn * WN + j * 32 + 8 * q + 4 * (lane >> 5);  // channel within the tile
+      const int n = n0 + nl;
+      const float4 swq = *reinterpret_cast<const float4*>(scale_lds + BM + nl);
+      const float sw4[4] = {swq.x, swq.y, swq.z, swq.w};
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int ml = wm * WM + i * 32 + (lane & 31);  // token within the tile
+        const int m = min(m0 + ml, M - 1);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = epilogue_value<RANK>(ep, acc[j][i][4 * q + e], m, min(n + e, N - 1), sxm[i], sw4[e]);
+        const int chunk = (nl >> 3) ^ (ml % OUT_CH);
+        *reinterpret_cast<uint2*>(lds + ml * (BN * 2) + chunk * 16 + (nl & 4) * 2) =
+            uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      }
+    }
+  }
+  lds_barrier();
+  const bool y_vec = ((ep.ldy | N) & 7) == 0 && (reinterpret_cast<uintptr_t>(ep.y) & 15) == 0;
+  constexpr int NT = 64 * NW;
+#pragma unroll 4
+  for (int c = threadIdx.x; c < BM * OUT_CH; c += NT) {
+    const int ml = c / OUT_CH, ch = c % OUT_CH;
+    const int m = m0 + ml, n = n0 + ch * 8;
+    if (m >= M || n >= N) continue;
+    const uint4 v = *reinterpret_cast<const uint4*>(lds + ml * (BN * 2) + (ch ^ (ml % OUT_CH)) * 16);
+    uint16_t* dst = ep.y + (int64_t)m * ep.ldy + n;
+    if (y_vec) {
+      *reinterpret_cast<uint4*>(dst) = v;
+    } else {
+      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (n + e < N) dst[e] = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+}
+
+template <int BM, int BN, int WGM, int WGN, int BK, int STAGES, int RANK, bool PACKW, bool PACKX>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint8_t* __restrict__ xq, int64_t ldx,
                                                                       const uint8_t* __restrict__ w, int64_t ldw, int M,
                                                                       int N, int K, int tiles_m, int tiles_n, int group_m,
@@ -103,9 +167,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
   static_assert(BK == 64 || BK == 128, "stage depth");
   static_assert(ROWS % (RPL * NW) == 0 && TM >= 1 && TN >= 1, "tile does not divide among the waves");
   static_assert(STAGES >= 3 && (STAGES - 2) * LOADS < 64, "pipeline depth");
-  constexpr int OUT_CH = BN * 2 / 16;          // 16-byte chunks per output tile row
   constexpr int LDS_BYTES = STAGES * STAGE > BM * BN * 2 ? STAGES * STAGE : BM * BN * 2;
-  static_assert(OUT_CH <= 32 && (OUT_CH & (OUT_CH - 1)) == 0, "output tile width");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
   __shared__ __attribute__((aligned(256))) float scale_lds[BM + BN];  // sx of the tile's tokens, then sw of its channels
 
@@ -129,15 +191,23 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
   // wave-load copies contiguous global memory (one 1 KB half, or two 512-byte
   // pieces) into its contiguous 1 KB of LDS. Each wave-load index i holds
   // only token rows or only weight data.
+  // Packed activation codes (PACKX, the same fragment order) are copied the
+  // same way into the token part of the stage.
   static_assert(BM % (NW * RPL) == 0, "wave-loads straddle the token/weight boundary");
-  const int ntiles = (N + 15) >> 4;
+  const int ntiles = (N + 15) >> 4, mtiles = (M + 15) >> 4;
   const uint8_t* src[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
     const int g = i * NW + wave;
     const int r = g * RPL + lane / CH;
     const int chunk = (lane % CH) ^ swizzle<BK>(r);
-    if (r < BM) {
+    if (r < BM && PACKX) {
+      const int tt = BK == 128 ? g >> 1 : g;
+      const int h = BK == 128 ? g & 1 : lane >> 5;
+      const int lp = BK == 128 ? lane : lane & 31;
+      const int tile = min((m0 >> 4) + tt, mtiles - 1);
+      src[i] = xq + (((int64_t)tile * (K >> 7)) * 2 + h) * 1024 + lp * 16;
+    } else if (r < BM) {
       src[i] = xq + (int64_t)min(m0 + r, M - 1) * ldx + chunk * 16;
     } else if (PACKW) {
       const int gw = g - BM / RPL;  // weight wave-load: tile gw (64-deep) or half gw%2 of tile gw/2
@@ -155,8 +225,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
     uint8_t* base = lds + (kt % STAGES) * STAGE;
     const int64_t k0 = (int64_t)kt * BK;
     const int64_t wk = PACKW ? tiled_stage_offset<BK>(kt) : k0;
+    const int64_t xk = PACKX ? tiled_stage_offset<BK>(kt) : k0;
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) load_lds16(src[i] + (i * NW * RPL < BM ? k0 : wk), base + (i * NW + wave) * 1024);
+    for (int i = 0; i < LOADS; ++i) load_lds16(src[i] + (i * NW * RPL < BM ? xk : wk), base + (i * NW + wave) * 1024);
   };
 
   f32x16 acc[TN][TM];
@@ -198,11 +269,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
   // rr%16 + 16*kh of the stage's piece (64-deep: halves 512 bytes apart, 1 KB
   // per tile). A 16-lane phase reads 256 consecutive bytes.
   constexpr int TSTRIDE = BK == 128 ? 2048 : 1024, HSTRIDE = BK == 128 ? 1024 : 512;
-  int aoff[TN];
+  int aoff[TN], boff[TM];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int rr = wn * WN + j * 32 + frow;
     aoff[j] = BM * BK + (rr >> 4) * TSTRIDE + ((rr & 15) + 16 * (lane >> 5)) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int rr = wm * WM + i * 32 + frow;
+    boff[i] = (rr >> 4) * TSTRIDE + ((rr & 15) + 16 * (lane >> 5)) * 16;
   }
   auto load_frags = [&](int kt, int s, i32x8 (&a)[TN], i32x8 (&b)[TM]) {
     const uint8_t* base = lds + (kt % STAGES) * STAGE;
@@ -219,9 +295,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      const int r = brow[i], sw = swizzle<BK>(r);
-      b[i] = cat8(lds_read16(base + r * BK + ((4 * s + fhalf) ^ sw) * 16),
-                  lds_read16(base + r * BK + ((4 * s + fhalf + 1) ^ sw) * 16));
+      if constexpr (PACKX) {
+        const uint8_t* p = base + boff[i] + s * 512;
+        b[i] = cat8(lds_read16(p), lds_read16(p + HSTRIDE));
+      } else {
+        const int r = brow[i], sw = swizzle<BK>(r);
+        b[i] = cat8(lds_read16(base + r * BK + ((4 * s + fhalf) ^ sw) * 16),
+                    lds_read16(base + r * BK + ((4 * s + fhalf + 1) ^ sw) * 16));
+      }
     }
   };
 
@@ -280,58 +361,185 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
     }
   }
 
-  // Epilogue. 32x32 MFMA output layout: lane l holds column l % 32 (a token)
-  // and, in register r, row 8*(r/4) + 4*(l/32) + r%4 (a channel): each register
-  // quad is 4 consecutive channels of one token. The finished bf16 tile goes
-  // through LDS ([BM tokens][BN channels], 16-byte chunk c of row r stored at
-  // chunk c ^ (r % OUT_CH)) so that global stores are 16 bytes per lane over
-  // whole row segments.
-  float sxm[TM];
+  store_tile<BM, BN, WGM, WGN, RANK>(lds, scale_lds, acc, ep, m0, n0, M, N, wm, wn, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Ping-pong form of the prefill GEMM for 64-deep stages and 8 waves (2 x 4).
+// The two waves that share a SIMD belong to different groups: group 0 (waves
+// 0-3, one per SIMD) and group 1 (waves 4-7). The groups take turns: while one
+// group issues the MFMAs of its step from registers, the other reads its next
+// step's fragments from LDS and issues its share of the global -> LDS copies;
+// every turn ends at a workgroup barrier. So the MFMA pipe of each SIMD has one
+// wave feeding it at a time, and the LDS reads never wait behind the MFMAs of
+// the same wave (in the lockstep form both waves of a SIMD read, then both
+// multiply).
+//
+// Turns (phases) P = 0 .. 2U-1 for U steps: group 0 computes step P/2 at
+// even P and reads step (P+1)/2 at odd P; group 1 computes step (P-1)/2 at odd
+// P and reads step P/2 at even P (it idles at P = 0, group 0 at P = 2U-1).
+// Stage j's LDS buffer is read by group 0 in phase 2j-1 and by group 1 in
+// phase 2j; in the read turn of step m each group copies its share of stage
+// m+STAGES-1 into the buffer of stage m-1, which both groups finished reading
+// by the end of phase 2m-2. Stage j must have landed (every wave's copies)
+// before phase 2j-1, so each wave waits for its own copies of stage j+1 before
+// the barrier that ends phase 2j.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int STAGES, int RANK, bool PACKW, bool PACKX>
+__global__ __launch_bounds__(512) void gemm_prefill_pp_kernel(const uint8_t* __restrict__ xq, int64_t ldx,
+                                                              const uint8_t* __restrict__ w, int64_t ldw, int M, int N,
+                                                              int K, int tiles_m, int tiles_n, int group_m, Epilogue ep) {
+  constexpr int WGM = 2, WGN = 4, NW = 8, BK = 64;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int CH = BK / 16, RPL = 1024 / BK;
+  constexpr int ROWS = BM + BN, STAGE = ROWS * BK;
+  constexpr int LOADS = ROWS / RPL / NW;  // wave-loads per wave per stage
+  static_assert(ROWS % (RPL * NW) == 0 && BM % (NW * RPL) == 0 && TM >= 1 && TN >= 1, "tile shape");
+  static_assert(STAGES >= 3 && STAGES <= 5 && (STAGES - 1) * LOADS < 64, "pipeline depth");
+  constexpr int LDS_BYTES = STAGES * STAGE > BM * BN * 2 ? STAGES * STAGE : BM * BN * 2;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+  __shared__ __attribute__((aligned(256))) float scale_lds[BM + BN];
+
+  int tile_m, tile_n;
+  tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tile_m, tile_n);
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int grp = wave >> 2;
+
+  // Copy assignment as in gemm_prefill_kernel (64-deep stages).
+  const int ntiles = (N + 15) >> 4, mtiles = (M + 15) >> 4;
+  const uint8_t* src[LOADS];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) sxm[i] = scale_lds[wm * WM + i * 32 + (lane & 31)];
-  // Every wave's operand reads are complete before the tile overwrites them.
-  lds_barrier();
+  for (int i = 0; i < LOADS; ++i) {
+    const int g = i * NW + wave;
+    const int r = g * RPL + lane / CH;
+    const int chunk = (lane % CH) ^ swizzle<BK>(r);
+    if (r < BM && PACKX) {
+      const int tile = min((m0 >> 4) + g, mtiles - 1);
+      src[i] = xq + (((int64_t)tile * (K >> 7)) * 2 + (lane >> 5)) * 1024 + (lane & 31) * 16;
+    } else if (r < BM) {
+      src[i] = xq + (int64_t)min(m0 + r, M - 1) * ldx + chunk * 16;
+    } else if (PACKW) {
+      const int tile = min((n0 >> 4) + (g - BM / RPL), ntiles - 1);
+      src[i] = w + (((int64_t)tile * (K >> 7)) * 2 + (lane >> 5)) * 1024 + (lane & 31) * 16;
+    } else {
+      src[i] = w + (int64_t)min(n0 + r - BM, N - 1) * ldw + chunk * 16;
+    }
+  }
+  auto issue_stage = [&](int kt) {
+    uint8_t* base = lds + (kt % STAGES) * STAGE;
+    const int64_t k0 = (int64_t)kt * BK;
+    const int64_t wk = PACKW ? tiled_stage_offset<BK>(kt) : k0;
+    const int64_t xk = PACKX ? tiled_stage_offset<BK>(kt) : k0;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) load_lds16(src[i] + (i * NW * RPL < BM ? xk : wk), base + (i * NW + wave) * 1024);
+  };
+  // Wait until at most `stages` later stages of this wave's copies are in flight.
+  auto wait_copies = [&](int stages) {
+    if (stages >= 3) wait_vmem_below<(STAGES > 3 ? 3 * LOADS : 0)>();
+    else if (stages == 2) wait_vmem_below<2 * LOADS>();
+    else if (stages == 1) wait_vmem_below<LOADS>();
+    else wait_vmem_below<0>();
+  };
+
+  f32x16 acc[TN][TM];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
+
+  for (int t = wave * 64; t < BM + BN; t += NW * 64) {
+    const int r = t + lane;
+    const float* sp = r < BM ? ep.sx + min(m0 + r, M - 1) : ep.sw + min(n0 + r - BM, N - 1);
+    typedef __attribute__((address_space(3))) void lds_void;
+    typedef __attribute__((address_space(1))) void global_void;
+    __builtin_amdgcn_global_load_lds((global_void*)sp, (lds_void*)(scale_lds + t), 4, 0, 0);
+  }
+
+  const int frow = lane & 31;
+  const int fhalf = (lane >> 5) * 2;
+  int brow[TM], boff[TM], aoff[TN], arow[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    brow[i] = wm * WM + i * 32 + frow;
+    boff[i] = (brow[i] >> 4) * 1024 + ((brow[i] & 15) + 16 * (lane >> 5)) * 16;
+  }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
+    arow[j] = BM + wn * WN + j * 32 + frow;
+    const int rr = wn * WN + j * 32 + frow;
+    aoff[j] = BM * BK + (rr >> 4) * 1024 + ((rr & 15) + 16 * (lane >> 5)) * 16;
+  }
+  i32x8 fa[TN], fb[TM];
+  auto load_frags = [&](int kt) {
+    const uint8_t* base = lds + (kt % STAGES) * STAGE;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int nl = wn * WN + j * 32 + 8 * q + 4 * (lane >> 5);  // channel within the tile
-      const int n = n0 + nl;
-      const float4 swq = *reinterpret_cast<const float4*>(scale_lds + BM + nl);
-      const float sw4[4] = {swq.x, swq.y, swq.z, swq.w};
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int ml = wm * WM + i * 32 + (lane & 31);  // token within the tile
-        const int m = min(m0 + ml, M - 1);
-        uint32_t h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          h[e] = f32_to_bf16(epilogue_value<RANK>(ep, acc[j][i][4 * q + e], m, min(n + e, N - 1), sxm[i], sw4[e]));
-        const int chunk = (nl >> 3) ^ (ml % OUT_CH);
-        *reinterpret_cast<uint2*>(lds + ml * (BN * 2) + chunk * 16 + (nl & 4) * 2) =
-            uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    for (int j = 0; j < TN; ++j) {
+      if constexpr (PACKW) {
+        const uint8_t* p = base + aoff[j];
+        fa[j] = cat8(lds_read16(p), lds_read16(p + 512));
+      } else {
+        const int r = arow[j], sw = swizzle<BK>(r);
+        fa[j] = cat8(lds_read16(base + r * BK + (fhalf ^ sw) * 16), lds_read16(base + r * BK + ((fhalf + 1) ^ sw) * 16));
       }
     }
-  }
-  lds_barrier();
-  const bool y_vec = ((ep.ldy | N) & 7) == 0 && (reinterpret_cast<uintptr_t>(ep.y) & 15) == 0;
-  constexpr int NT = 64 * NW;
-#pragma unroll 4
-  for (int c = threadIdx.x; c < BM * OUT_CH; c += NT) {
-    const int ml = c / OUT_CH, ch = c % OUT_CH;
-    const int m = m0 + ml, n = n0 + ch * 8;
-    if (m >= M || n >= N) continue;
-    const uint4 v = *reinterpret_cast<const uint4*>(lds + ml * (BN * 2) + (ch ^ (ml % OUT_CH)) * 16);
-    uint16_t* dst = ep.y + (int64_t)m * ep.ldy + n;
-    if (y_vec) {
-      *reinterpret_cast<uint4*>(dst) = v;
-    } else {
-      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (n + e < N) dst[e] = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
+    for (int i = 0; i < TM; ++i) {
+      if constexpr (PACKX) {
+        fb[i] = cat8(lds_read16(base + boff[i]), lds_read16(base + boff[i] + 512));
+      } else {
+        const int r = brow[i], sw = swizzle<BK>(r);
+        fb[i] = cat8(lds_read16(base + r * BK + (fhalf ^ sw) * 16), lds_read16(base + r * BK + ((fhalf + 1) ^ sw) * 16));
+      }
+    }
+  };
+
+  const int U = K / BK;
+#pragma unroll
+  for (int p = 0; p < STAGES; ++p)
+    if (p < U) issue_stage(p);
+  wait_copies(min(STAGES - 1, U - 1));  // stage 0 (and the scales) landed
+  barrier_only();
+  load_frags(0);
+  if (grp == 1) {
+    // Phase 0 is group 0's first compute turn; group 1 only waits for stage 1
+    // and finishes its reads of stage 0 (that buffer is refilled in phase 1).
+    if (U > 1) wait_copies(min(STAGES - 2, U - 2));
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    barrier_only();
+  }
+  for (int k = 0; k < U; ++k) {
+    // Compute turn of step k, from the fragments read in the previous turn.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) acc[j][i] = mfma_32x32x64_fp8(fa[j], fb[i], acc[j][i]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (grp == 0 && k + 1 < U) wait_copies(min(STAGES - 2, U - 2 - k));
+    barrier_only();
+    // Read turn of step k+1 (group 0 ends with an idle turn that matches
+    // group 1's last compute turn).
+    if (k + 1 < U) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (k + STAGES < U) issue_stage(k + STAGES);
+      load_frags(k + 1);
+      if (grp == 1 && k + 2 < U) wait_copies(min(STAGES - 2, U - 3 - k));
+      // This turn's LDS reads are complete before the barrier: the buffer is
+      // refilled by the other group's next read turn.
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_sched_barrier(0);
+      barrier_only();
+    } else if (grp == 0) {
+      barrier_only();
     }
   }
+  store_tile<BM, BN, WGM, WGN, RANK>(lds, scale_lds, acc, ep, m0, n0, M, N, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -520,32 +728,60 @@ hipError_t w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64
   return launch_w8a16_prefill<128, 128, 2, 2, 3>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 8, stream);
 }
 
+// ldx = 0: activation codes in the packed fragment order (packed_x_offset);
+// ldw = 0: tiled weights (tiled_w_offset).
 template <int BM, int BN, int WGM, int WGN, int BK, int STAGES>
 static hipError_t launch_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
                                  const Epilogue& ep, int rank, int group_m, hipStream_t stream) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
   const dim3 grid((unsigned)(tm * tn)), block(64 * WGM * WGN);
   if (group_m < 1) group_m = 1;
-#define JV_PREFILL_LAUNCH(R, PW)                                   \
-  gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, R, PW>         \
+#define JV_PREFILL_LAUNCH(R, PW, PX)                                   \
+  gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, R, PW, PX>         \
       <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep)
+#define JV_PREFILL_LAUNCH_X(R, PW)             \
+  if (ldx == 0) JV_PREFILL_LAUNCH(R, PW, true); \
+  else JV_PREFILL_LAUNCH(R, PW, false);
   if (rank == 16) {
-    if (ldw == 0) JV_PREFILL_LAUNCH(16, true);
-    else JV_PREFILL_LAUNCH(16, false);
+    if (ldw == 0) { JV_PREFILL_LAUNCH_X(16, true) }
+    else { JV_PREFILL_LAUNCH_X(16, false) }
   } else {
-    if (ldw == 0) JV_PREFILL_LAUNCH(0, true);
-    else JV_PREFILL_LAUNCH(0, false);
+    if (ldw == 0) { JV_PREFILL_LAUNCH_X(0, true) }
+    else { JV_PREFILL_LAUNCH_X(0, false) }
   }
+#undef JV_PREFILL_LAUNCH_X
 #undef JV_PREFILL_LAUNCH
   return hipGetLastError();
 }
 
+// The ping-pong form (no LoRA epilogue: with it the kernel needs more than
+// the 256 registers two waves per SIMD leave each wave).
+template <int BM, int BN, int STAGES>
+static hipError_t launch_prefill_pp(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                                    const Epilogue& ep, int group_m, hipStream_t stream) {
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  const dim3 grid((unsigned)(tm * tn)), block(512);
+  if (group_m < 1) group_m = 1;
+#define JV_PREFILL_PP_LAUNCH(PW, PX) \
+  gemm_prefill_pp_kernel<BM, BN, STAGES, 0, PW, PX><<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep)
+  if (ldw == 0) {
+    if (ldx == 0) JV_PREFILL_PP_LAUNCH(true, true);
+    else JV_PREFILL_PP_LAUNCH(true, false);
+  } else {
+    if (ldx == 0) JV_PREFILL_PP_LAUNCH(false, true);
+    else JV_PREFILL_PP_LAUNCH(false, false);
+  }
+#undef JV_PREFILL_PP_LAUNCH
+  return hipGetLastError();
+}
+
 PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count) {
-  // 256x256 tiles (least L2 -> LDS traffic per flop) when they give every CU
-  // at least two; else 256x128 when those give every CU one; else 128x128.
-  // Measured on MI355X over the 9B projection shapes at M = 512..8192.
+  // 256x256 tiles (least L2 -> LDS traffic per flop, in the ping-pong form)
+  // when they give every CU at least two; else 256x128 when those give every
+  // CU one; else 128x128. Measured on MI355X over the 9B projection shapes at
+  // M = 512..8192.
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-  if (t256 >= 2 * (int64_t)cu_count) return PrefillTile{256, 256, 2, 4, 64, 4, 4};
+  if (t256 >= 2 * (int64_t)cu_count) return PrefillTile{256, 256, 2, 4, 64, 4, 4, true};
   const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
   if (t256x128 >= cu_count) return PrefillTile{256, 128, 2, 4, 128, 3, 4};
   return PrefillTile{128, 128, 2, 2, 128, 4, 8};
@@ -554,25 +790,36 @@ PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count) {
 hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
                         const Epilogue& ep, int rank, PrefillTile t, hipStream_t stream) {
   if (rank != 0 && rank != 16) return hipErrorInvalidValue;
-  if (K % t.bk) return hipErrorInvalidValue;
+  if (K % t.bk || K % 128) return hipErrorInvalidValue;
+  if (t.pingpong && rank == 0) {
+    if (t.wgm != 2 || t.wgn != 4 || t.bk != 64) return hipErrorInvalidValue;
+#define JV_PREFILL_PP_CASE(BM_, BN_, ST_) \
+  if (t.bm == BM_ && t.bn == BN_ && t.stages == ST_) \
+    return launch_prefill_pp<BM_, BN_, ST_>(xq, ldx, w, ldw, M, N, K, ep, t.group_m, stream);
+    JV_PREFILL_PP_CASE(256, 256, 4)
+#ifdef JV_PREFILL_ALL_TILES
+    JV_PREFILL_PP_CASE(256, 256, 3)
+    JV_PREFILL_PP_CASE(256, 128, 4)
+#endif
+#undef JV_PREFILL_PP_CASE
+    return hipErrorInvalidValue;
+  }
+  // With a LoRA epilogue the 256x256 tile needs more registers than two waves
+  // per SIMD leave each wave: such launches take 256x128 tiles.
+  if (t.pingpong || (rank == 16 && t.bm == 256 && t.bn == 256)) t = PrefillTile{256, 128, 2, 4, 128, 3, 4};
 #define JV_PREFILL_CASE(BM_, BN_, WGM_, WGN_, BK_, ST_)                                                     \
   if (t.bm == BM_ && t.bn == BN_ && t.wgm == WGM_ && t.wgn == WGN_ && t.bk == BK_ && t.stages == ST_)       \
     return launch_prefill<BM_, BN_, WGM_, WGN_, BK_, ST_>(xq, ldx, w, ldw, M, N, K, ep, rank, t.group_m, stream);
-  // The shapes prefill_tile picks.
-  JV_PREFILL_CASE(256, 256, 2, 4, 64, 4)
+  // The lockstep shapes prefill_tile picks.
   JV_PREFILL_CASE(256, 128, 2, 4, 128, 3)
   JV_PREFILL_CASE(128, 128, 2, 2, 128, 4)
 #ifdef JV_PREFILL_ALL_TILES
   // Further shapes for launch-shape sweeps.
-  JV_PREFILL_CASE(256, 256, 4, 2, 64, 3)
+  JV_PREFILL_CASE(256, 256, 2, 4, 64, 4)
   JV_PREFILL_CASE(256, 256, 4, 2, 64, 4)
   JV_PREFILL_CASE(256, 256, 2, 4, 64, 3)
-  JV_PREFILL_CASE(256, 128, 4, 2, 128, 3)
   JV_PREFILL_CASE(256, 128, 2, 4, 64, 4)
-  JV_PREFILL_CASE(256, 128, 4, 2, 64, 4)
   JV_PREFILL_CASE(128, 256, 2, 4, 128, 3)
-  JV_PREFILL_CASE(128, 256, 2, 4, 64, 4)
-  JV_PREFILL_CASE(128, 128, 2, 2, 128, 3)
   JV_PREFILL_CASE(128, 128, 2, 2, 64, 4)
 #endif
 #undef JV_PREFILL_CASE

@@ -21,15 +21,19 @@ struct DecodePlan {
 
 // Prefill launch shape: output tile bm (tokens) x bn (channels), a wgm x wgn
 // grid of waves per workgroup, K stages of bk bytes in a ring of `stages` LDS
-// buffers, and group_m M-tiles walking N together.
+// buffers, and group_m M-tiles walking N together. pingpong selects the form
+// whose two wave groups alternate MFMAs and LDS reads (2 x 4 waves, bk = 64).
 struct PrefillTile {
   int bm, bn, wgm, wgn, bk, stages, group_m;
+  bool pingpong = false;
 };
 
-// Byte offset of activation code (m, k) in the packed decode layout: for
-// token tile mt = m/16 and 128-k step s, two 1 KB halves, each holding 16
-// bytes per lane in MFMA B-fragment order (lane = m%16 + 16*((k%128)/32),
-// half = (k%32)/16). Rows are padded to a multiple of 16 tokens.
+// Byte offset of activation code (m, k) in the packed layout: for token tile
+// mt = m/16 and 128-k step s, two 1 KB halves, each holding 16 bytes per lane
+// in the decode MFMA's B-fragment order (lane = m%16 + 16*((k%128)/32),
+// half = (k%32)/16). Rows are padded to a multiple of 16 tokens. The prefill
+// kernels copy the same 512-byte runs (half a fragment per 64-deep stage)
+// into LDS and read their 32x32x64 fragments from them.
 __host__ __device__ inline int64_t packed_x_offset(int m, int k, int ksteps) {
   const int mt = m >> 4, s = k >> 7, kk = k & 127;
   const int lane = (m & 15) + 16 * (kk >> 5), half = (kk >> 4) & 1;
@@ -51,8 +55,8 @@ hipError_t tile_weight(const uint8_t* codes, int64_t ldc, int N, int K, uint8_t*
 hipError_t untile_weight(const uint8_t* tiled, int N, int K, uint8_t* codes, int64_t ldc, hipStream_t stream);
 
 int quant_chunks(int K);
-// packed: write codes in the packed decode layout (codes sized
-// packed_x_bytes(M, K), ldc ignored; the padding rows get zero codes).
+// packed: write codes in the packed layout (codes sized packed_x_bytes(M, K),
+// ldc ignored; the padding rows get zero codes).
 hipError_t quant_rows_bf16(const uint16_t* x, int64_t ldx, int64_t M, int K, uint8_t* codes, int64_t ldc, float* scales,
                            const uint16_t* lora_a, int rank, float* lora_t, bool packed, hipStream_t stream);
 hipError_t quant_swiglu_bf16(const uint16_t* gate, int64_t ldg, const uint16_t* up, int64_t ldu, int64_t M, int K,
@@ -67,6 +71,7 @@ hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, bool packed_x, const uin
                        hipStream_t stream);
 
 PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count);
+// ldx = 0: packed activation codes (packed_x_offset); ldw = 0: tiled weights.
 hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
                         const Epilogue& ep, int rank, PrefillTile tile, hipStream_t stream);
 

@@ -24,15 +24,29 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
   return v;
 }
 
+// Packed codes of more than one 16-token tile: the 16 rows of a tile are
+// quantized on one XCD (the hardware hands consecutive workgroups to the 8
+// XCDs in turn), so the 16-byte pieces they write into each fragment meet in
+// one L2 and reach memory as whole lines. Workgroup b serves row 16 t + j % 16
+// of tile t = b % 8 + 8 (j / 16), j = b / 8; -1 past the last tile.
+__device__ __forceinline__ int packed_tile_row(int b, int tiles) {
+  const int j = b >> 3;
+  const int t = (b & 7) + 8 * (j >> 4);
+  return t < tiles ? t * 16 + (j & 15) : -1;
+}
+
 // NC chunks of 8 elements per thread kept in registers (K <= NC * 8 * THREADS).
-template <int THREADS, int NC, bool SWIGLU, int RANK, bool PACKED>
+// XCD_ROWS: workgroups map to rows through packed_tile_row.
+template <int THREADS, int NC, bool SWIGLU, int RANK, bool PACKED, bool XCD_ROWS = false>
 __global__ __launch_bounds__(THREADS) void quant_rows_bf16_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ up, int64_t ldu, int K, int M,
     uint8_t* __restrict__ codes, int64_t ldc, float* __restrict__ scales, uint16_t* __restrict__ h_out, int64_t ldh,
     const uint16_t* __restrict__ lora_a, float* __restrict__ lora_t) {
   __shared__ uint32_t lds[quant_row_lds_bytes<THREADS, RANK>() / 4];
-  quant_row<THREADS, NC, SWIGLU, RANK, PACKED>((int)blockIdx.x, x, ldx, up, ldu, K, M, codes, ldc, scales, h_out, ldh,
-                                               lora_a, lora_t, lds);
+  const int row = XCD_ROWS ? packed_tile_row((int)blockIdx.x, (M + 15) >> 4) : (int)blockIdx.x;
+  if (row < 0) return;
+  quant_row<THREADS, NC, SWIGLU, RANK, PACKED>(row, x, ldx, up, ldu, K, M, codes, ldc, scales, h_out, ldh, lora_a, lora_t,
+                                               lds);
 }
 
 // Rows longer than the register cache: two passes over the row (the second
@@ -112,22 +126,23 @@ int quant_chunks(int K) {
   return 0;
 }
 
-template <bool SWIGLU, int RANK, bool PACKED = false>
-static hipError_t launch_rows(int shape, const uint16_t* x, int64_t ldx, const uint16_t* up, int64_t ldu, int64_t M, int K,
-                              uint8_t* codes, int64_t ldc, float* scales, uint16_t* h_out, int64_t ldh,
-                              const uint16_t* lora_a, float* lora_t, hipStream_t stream) {
-  const dim3 grid((unsigned)(PACKED ? (M + 15) / 16 * 16 : M));
+template <bool SWIGLU, int RANK, bool PACKED, bool XCD_ROWS>
+static hipError_t launch_rows_grid(int shape, const uint16_t* x, int64_t ldx, const uint16_t* up, int64_t ldu, int64_t M,
+                                   int K, uint8_t* codes, int64_t ldc, float* scales, uint16_t* h_out, int64_t ldh,
+                                   const uint16_t* lora_a, float* lora_t, hipStream_t stream) {
+  const int64_t tiles = (M + 15) / 16;
+  const dim3 grid((unsigned)(XCD_ROWS ? (tiles + 7) / 8 * 128 : PACKED ? tiles * 16 : M));
   switch (shape) {
     case 1:
-      quant_rows_bf16_kernel<512, 1, SWIGLU, RANK, PACKED>
+      quant_rows_bf16_kernel<512, 1, SWIGLU, RANK, PACKED, XCD_ROWS>
           <<<grid, dim3(512), 0, stream>>>(x, ldx, up, ldu, K, (int)M, codes, ldc, scales, h_out, ldh, lora_a, lora_t);
       break;
     case 2:
-      quant_rows_bf16_kernel<1024, 1, SWIGLU, RANK, PACKED>
+      quant_rows_bf16_kernel<1024, 1, SWIGLU, RANK, PACKED, XCD_ROWS>
           <<<grid, dim3(1024), 0, stream>>>(x, ldx, up, ldu, K, (int)M, codes, ldc, scales, h_out, ldh, lora_a, lora_t);
       break;
     case 3:
-      quant_rows_bf16_kernel<1024, 2, SWIGLU, RANK, PACKED>
+      quant_rows_bf16_kernel<1024, 2, SWIGLU, RANK, PACKED, XCD_ROWS>
           <<<grid, dim3(1024), 0, stream>>>(x, ldx, up, ldu, K, (int)M, codes, ldc, scales, h_out, ldh, lora_a, lora_t);
       break;
     default:
@@ -136,12 +151,25 @@ static hipError_t launch_rows(int shape, const uint16_t* x, int64_t ldx, const u
   return hipGetLastError();
 }
 
+// Packed codes of prefill batches (more than kDecodeMaxRows rows) group each
+// tile's rows on one XCD; decode batches keep one workgroup per row.
+template <bool SWIGLU, int RANK, bool PACKED = false>
+static hipError_t launch_rows(int shape, const uint16_t* x, int64_t ldx, const uint16_t* up, int64_t ldu, int64_t M, int K,
+                              uint8_t* codes, int64_t ldc, float* scales, uint16_t* h_out, int64_t ldh,
+                              const uint16_t* lora_a, float* lora_t, hipStream_t stream) {
+  if (PACKED && M > kDecodeMaxRows)
+    return launch_rows_grid<SWIGLU, RANK, PACKED, true>(shape, x, ldx, up, ldu, M, K, codes, ldc, scales, h_out, ldh, lora_a,
+                                                        lora_t, stream);
+  return launch_rows_grid<SWIGLU, RANK, PACKED, false>(shape, x, ldx, up, ldu, M, K, codes, ldc, scales, h_out, ldh, lora_a,
+                                                       lora_t, stream);
+}
+
 hipError_t quant_rows_bf16(const uint16_t* x, int64_t ldx, int64_t M, int K, uint8_t* codes, int64_t ldc, float* scales,
                            const uint16_t* lora_a, int rank, float* lora_t, bool packed, hipStream_t stream) {
   if (M == 0) return hipSuccess;
   const int nc = quant_chunks(K);
   if (packed) {
-    if (nc == 0 || M > kDecodeMaxRows || (K & 127)) return hipErrorInvalidValue;
+    if (nc == 0 || (K & 127)) return hipErrorInvalidValue;
     if (rank == 16)
       return launch_rows<false, 16, true>(nc, x, ldx, nullptr, 0, M, K, codes, 0, scales, nullptr, 0, lora_a, lora_t, stream);
     if (rank == 0)
@@ -167,7 +195,7 @@ hipError_t quant_swiglu_bf16(const uint16_t* gate, int64_t ldg, const uint16_t* 
   const int nc = quant_chunks(K);
   if (nc == 0) return hipErrorInvalidValue;
   if (packed) {
-    if (M > kDecodeMaxRows || (K & 127)) return hipErrorInvalidValue;
+    if (K & 127) return hipErrorInvalidValue;
     if (rank == 0)
       return launch_rows<true, 0, true>(nc, gate, ldg, up, ldu, M, K, codes, 0, scales, h_out, ldh, nullptr, nullptr, stream);
     if (rank == 16)

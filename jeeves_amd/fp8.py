@@ -31,6 +31,8 @@ from .fp8_weights import FP8, quantize_rows
 # Rows at or below which fp8_matmul takes the decode kernel (the role of
 # SPLIT_K_MAX_ROWS, inference/fp8.py:20): up to four 16-token MFMA column tiles.
 DECODE_MAX_ROWS = 64
+# Longest row the single-pass quantizer (and so the packed code layout) covers.
+QUANT_MAX_PACKED_COLS = 16384
 BLOCK_K = 128
 TILE_COUNTER_SLOTS = 1 << 16
 # One row count per kernel variant: 1-4 decode token tiles, then prefill
@@ -228,12 +230,11 @@ def fp8_matmul_w8a16(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
 
 
 def packed_codes_bytes(rows: int, cols: int) -> int:
-    """Bytes of ``rows x cols`` activation codes in the decode GEMM's packed
-    fragment order (rows <= ``DECODE_MAX_ROWS``, cols a multiple of 128)."""
+    """Bytes of ``rows x cols`` activation codes in the GEMMs' packed fragment
+    order (cols a multiple of 128; rows padded to a multiple of 16)."""
     n = _lib.lib().jv_fp8_packed_codes_bytes(rows, cols)
     if n < 0:
-        raise ValueError(f"the packed layout takes at most {DECODE_MAX_ROWS} rows and a multiple of {BLOCK_K} columns, "
-                         f"got {rows} x {cols}")
+        raise ValueError(f"the packed layout takes a multiple of {BLOCK_K} columns, got {rows} x {cols}")
     return n
 
 
@@ -292,8 +293,8 @@ def swiglu_quantize(gate: torch.Tensor, up: torch.Tensor, *, lora_a: torch.Tenso
     """``h = F.silu(gate) * up`` on bf16 (``model/model.py:583``) fused with the
     down projection's per-token quantization. Returns ``(codes, scales)``, plus
     ``t = h A^T`` (float32 [M,r]) when ``lora_a`` is given and ``h`` (bf16) when
-    ``return_h``. ``packed``: codes come as a flat uint8 buffer in the decode
-    GEMM's fragment order, for ``fp8_matmul_quantized(..., packed_rows=M)``."""
+    ``return_h``. ``packed``: codes come as a flat uint8 buffer in the GEMMs'
+    fragment order, for ``fp8_matmul_quantized(..., packed_rows=M)``."""
     M, I = gate.shape
     if up.shape != gate.shape:
         raise ValueError(f"gate {tuple(gate.shape)} and up {tuple(up.shape)} differ")
@@ -454,8 +455,10 @@ class FP8SwiGLU(nn.Module):
             y = fp8_matmul_w8a16(h, self.down.weight, self.down.scale, bias=self.down.bias, tiled=self.down.tiled)
             return y.view(*shape[:-1], self.down.out_features)
         lora_a = self.down.lora[0] if self.down.lora is not None else None
-        # Decode batches hand the down GEMM its codes in fragment order.
-        packed = 0 < M <= DECODE_MAX_ROWS and inter % BLOCK_K == 0
+        # The down GEMM reads its codes fastest in fragment order (both the
+        # decode and the prefill kernels); the fused quantizer writes them so
+        # for rows up to 16384 channels.
+        packed = M > 0 and inter % BLOCK_K == 0 and inter <= QUANT_MAX_PACKED_COLS
         out = swiglu_quantize(gu[:, :inter], gu[:, inter:], lora_a=lora_a, packed=packed)
         lora_t = out[2] if lora_a is not None else None
         y = fp8_matmul_quantized(out[0], out[1], self.down.weight, self.down.scale, bias=self.down.bias, lora_t=lora_t,

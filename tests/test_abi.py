@@ -92,7 +92,9 @@ def test_packed_layout_sizes_are_host_logic(product_lib):
     assert L.jv_fp8_packed_codes_bytes(16, 4096) == 16 * 4096
     assert L.jv_fp8_packed_codes_bytes(17, 4096) == 32 * 4096   # rows pad to 16
     assert L.jv_fp8_packed_codes_bytes(1, 128) == 16 * 128
-    assert L.jv_fp8_packed_codes_bytes(65, 4096) == -1          # decode batches only
+    assert L.jv_fp8_packed_codes_bytes(65, 4096) == 80 * 4096   # prefill batches too
+    assert L.jv_fp8_packed_codes_bytes(2048, 12288) == 2048 * 12288
+    assert L.jv_fp8_packed_codes_bytes(-1, 4096) == -1
     assert L.jv_fp8_packed_codes_bytes(16, 100) == -1           # K must be a multiple of 128
 
 

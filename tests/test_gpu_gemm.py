@@ -17,7 +17,7 @@ import torch
 
 import oracle
 from jeeves_amd import _lib, synthetic
-from jeeves_amd.fp8 import fp8_matmul, fp8_matmul_quantized, swiglu_quantize
+from jeeves_amd.fp8 import fp8_matmul, fp8_matmul_quantized, swiglu_quantize, tile_weight
 from jeeves_amd.fp8_weights import FP8, quantize_rows
 from tests import helpers
 
@@ -259,6 +259,38 @@ def test_packed_activation_codes(M, N, K):
     check(y_packed, x, wq, sw)
     # padding rows of the last 16-token tile hold zero codes
     assert int(packed.long().sum().item()) == int(xq.view(torch.uint8).long().sum().item())
+
+
+# Prefill batches over every prefill kernel form: 256x256 tiles (ping-pong
+# form; M = 1993 leaves a partial last 16-token tile), 256x128 and 128x128.
+@pytest.mark.parametrize("M,N,K", [(2048, 24576, 4096), (1993, 24576, 4096), (2048, 4096, 12288), (300, 1024, 4096),
+                                   (65, 4096, 4096)])
+def test_packed_activation_codes_prefill(M, N, K):
+    """Packed codes (ldc = 0, ldxq = 0) through the prefill kernels give the
+    row-major codes' output bit for bit; sampled rows meet the oracle."""
+    from jeeves_amd.fp8 import packed_codes_bytes
+
+    x = synthetic.activations_heavy_tail(M, K, 140 + M).cuda()
+    wq, sw = quantize_rows(synthetic.weight(N, K, 141).cuda())
+    xq, sx = quantize_rows(x)
+    packed = torch.full((packed_codes_bytes(M, K),), 0xAA, dtype=torch.uint8, device="cuda")
+    psx = torch.empty(M, device="cuda")
+    _lib.check(_lib.lib().jv_fp8_quantize_rows_bf16(x.data_ptr(), K, M, K, packed.data_ptr(), 0, psx.data_ptr(),
+                                                    helpers.stream()))
+    assert torch.equal(psx, sx)
+    # the packed order is the tiled weight order applied to token rows, with
+    # zero codes in the padding rows of the last 16-token tile
+    padded = torch.zeros((M + 15) // 16 * 16, K, dtype=torch.uint8, device="cuda")
+    padded[:M] = xq.view(torch.uint8)
+    assert torch.equal(tile_weight(padded).view(torch.uint8).reshape(-1), packed)
+    for tiled in (False, True):
+        w = tile_weight(wq) if tiled else wq
+        y_row = fp8_matmul_quantized(xq, sx, w, sw, tiled=tiled)
+        y_packed = fp8_matmul_quantized(packed, psx, w, sw, packed_rows=M, tiled=tiled)
+        assert torch.equal(y_row, y_packed), tiled
+    assert torch.equal(fp8_matmul(x, wq, sw), y_packed)
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(M))[:48].sort().values.cuda()
+    check(y_packed[rows], x[rows], wq, sw)
 
 
 @pytest.mark.parametrize("M", [1, 16, 40])
