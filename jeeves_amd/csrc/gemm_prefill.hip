@@ -776,15 +776,22 @@ static hipError_t launch_prefill_pp(const uint8_t* xq, int64_t ldx, const uint8_
 }
 
 PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count) {
-  // 256x256 tiles (least L2 -> LDS traffic per flop, in the ping-pong form)
-  // when they give every CU at least two; else 256x128 when those give every
-  // CU one; else 128x128. Measured on MI355X over the 9B projection shapes at
-  // M = 512..8192.
+  // The largest tile that still gives every CU whole rounds of work: 256x256
+  // (least L2 -> LDS traffic per flop, in the ping-pong form) at two or more
+  // per CU; 256x128 at one per CU or two or more; 128x128 at two or more;
+  // else 64x64, whose 64 KB of LDS lets two workgroups share a CU (one's
+  // prologue and epilogue overlap the other's main loop). Measured on MI355X
+  // over the 9B projection shapes at M = 512, 2048 and 8192: k/v at M = 2048
+  // 21.9 -> 15.3 us with 64x64 instead of 128x128, gate+up at M = 512 73.5
+  // -> 70.0 us with 128x128 (three per CU) instead of 256x128 (one and a half).
+  const int64_t cus = cu_count;
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-  if (t256 >= 2 * (int64_t)cu_count) return PrefillTile{256, 256, 2, 4, 64, 4, 4, true};
+  if (t256 >= 2 * cus) return PrefillTile{256, 256, 2, 4, 64, 4, 4, true};
   const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
-  if (t256x128 >= cu_count) return PrefillTile{256, 128, 2, 4, 128, 3, 4};
-  return PrefillTile{128, 128, 2, 2, 128, 4, 8};
+  if (t256x128 == cus || t256x128 >= 2 * cus) return PrefillTile{256, 128, 2, 4, 128, 3, 4};
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  if (t128 >= 2 * cus) return PrefillTile{128, 128, 2, 2, 128, 4, 8};
+  return PrefillTile{64, 64, 2, 2, 128, 4, 8};
 }
 
 hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
@@ -813,6 +820,7 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
   // The lockstep shapes prefill_tile picks.
   JV_PREFILL_CASE(256, 128, 2, 4, 128, 3)
   JV_PREFILL_CASE(128, 128, 2, 2, 128, 4)
+  JV_PREFILL_CASE(64, 64, 2, 2, 128, 4)
 #ifdef JV_PREFILL_ALL_TILES
   // Further shapes for launch-shape sweeps.
   JV_PREFILL_CASE(256, 256, 2, 4, 64, 4)
@@ -821,6 +829,15 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
   JV_PREFILL_CASE(256, 128, 2, 4, 64, 4)
   JV_PREFILL_CASE(128, 256, 2, 4, 128, 3)
   JV_PREFILL_CASE(128, 128, 2, 2, 64, 4)
+  JV_PREFILL_CASE(128, 64, 2, 2, 128, 4)
+  JV_PREFILL_CASE(64, 128, 2, 2, 128, 4)
+  JV_PREFILL_CASE(128, 64, 4, 1, 128, 4)
+  JV_PREFILL_CASE(64, 64, 2, 2, 128, 3)
+  JV_PREFILL_CASE(128, 64, 2, 2, 128, 3)
+  JV_PREFILL_CASE(128, 128, 2, 2, 64, 3)
+  JV_PREFILL_CASE(256, 128, 2, 4, 64, 3)
+  JV_PREFILL_CASE(64, 128, 2, 2, 128, 3)
+  JV_PREFILL_CASE(64, 64, 2, 2, 64, 4)
 #endif
 #undef JV_PREFILL_CASE
   return hipErrorInvalidValue;
