@@ -118,12 +118,26 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_f32_kernel(const flo
 
 // Register-path shape for rows of K elements: 1 = 512 threads x 1 chunk
 // (K <= 4096), 2 = 1024 x 1 (K <= 8192), 3 = 1024 x 2 (K <= 16384); 0 when
-// the row needs the two-pass kernel.
+// the row needs the two-pass kernel. These minimise one row's latency (the
+// encode is on each thread's critical path), which is what decode batches
+// see.
 int quant_chunks(int K) {
   if (K <= 4096) return 1;
   if (K <= 8192) return 2;
   if (K <= 16384) return 3;
   return 0;
+}
+
+// Shape for batches of more than kDecodeMaxRows rows, where throughput
+// counts: 256 threads x NC chunks (NC = 1, 2, 4, 6, 8 for K up to 2048, 4096,
+// 8192, 12288, 16384): more rows resident per CU and NC loads in flight per
+// thread.
+static int quant_wide_shape(int K) {
+  if (K <= 2048) return 4;
+  if (K <= 4096) return 5;
+  if (K <= 8192) return 6;
+  if (K <= 12288) return 7;
+  return 8;
 }
 
 template <bool SWIGLU, int RANK, bool PACKED, bool XCD_ROWS>
@@ -145,6 +159,17 @@ static hipError_t launch_rows_grid(int shape, const uint16_t* x, int64_t ldx, co
       quant_rows_bf16_kernel<1024, 2, SWIGLU, RANK, PACKED, XCD_ROWS>
           <<<grid, dim3(1024), 0, stream>>>(x, ldx, up, ldu, K, (int)M, codes, ldc, scales, h_out, ldh, lora_a, lora_t);
       break;
+#define JV_QUANT_WIDE(SHAPE, NC)                                                                                         \
+    case SHAPE:                                                                                                         \
+      quant_rows_bf16_kernel<256, NC, SWIGLU, RANK, PACKED, XCD_ROWS>                                                   \
+          <<<grid, dim3(256), 0, stream>>>(x, ldx, up, ldu, K, (int)M, codes, ldc, scales, h_out, ldh, lora_a, lora_t); \
+      break;
+      JV_QUANT_WIDE(4, 1)
+      JV_QUANT_WIDE(5, 2)
+      JV_QUANT_WIDE(6, 4)
+      JV_QUANT_WIDE(7, 6)
+      JV_QUANT_WIDE(8, 8)
+#undef JV_QUANT_WIDE
     default:
       return hipErrorInvalidValue;
   }
@@ -157,6 +182,7 @@ template <bool SWIGLU, int RANK, bool PACKED = false>
 static hipError_t launch_rows(int shape, const uint16_t* x, int64_t ldx, const uint16_t* up, int64_t ldu, int64_t M, int K,
                               uint8_t* codes, int64_t ldc, float* scales, uint16_t* h_out, int64_t ldh,
                               const uint16_t* lora_a, float* lora_t, hipStream_t stream) {
+  if (M > kDecodeMaxRows) shape = quant_wide_shape(K);
   if (PACKED && M > kDecodeMaxRows)
     return launch_rows_grid<SWIGLU, RANK, PACKED, true>(shape, x, ldx, up, ldu, M, K, codes, ldc, scales, h_out, ldh, lora_a,
                                                         lora_t, stream);
