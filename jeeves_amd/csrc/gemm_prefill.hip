@@ -776,17 +776,19 @@ static hipError_t launch_prefill_pp(const uint8_t* xq, int64_t ldx, const uint8_
 }
 
 PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count) {
-  // The largest tile that still gives every CU whole rounds of work: 256x256
-  // (least L2 -> LDS traffic per flop, in the ping-pong form) at two or more
-  // per CU; 256x128 at one per CU or two or more; 128x128 at two or more;
-  // else 64x64, whose 64 KB of LDS lets two workgroups share a CU (one's
-  // prologue and epilogue overlap the other's main loop). Measured on MI355X
-  // over the 9B projection shapes at M = 512, 2048 and 8192: k/v at M = 2048
-  // 21.9 -> 15.3 us with 64x64 instead of 128x128, gate+up at M = 512 73.5
-  // -> 70.0 us with 128x128 (three per CU) instead of 256x128 (one and a half).
+  // 256x256 tiles in the ping-pong form (least L2 -> LDS traffic per flop,
+  // and the fastest tile per CU) once they cover five eighths of the CUs,
+  // even in a partial round; else the largest lockstep tile that gives every
+  // CU whole rounds of work: 256x128 at one per CU or two or more, 128x128 at
+  // two or more, else 64x64, whose 64 KB of LDS lets two workgroups share a CU
+  // (one's prologue and epilogue overlap the other's main loop). Measured on
+  // MI355X over the 9B projection shapes at M = 512, 2048 and 8192: gate+up
+  // at M = 512 (192 tiles of 256x256) 52.7 us against 72 us with 128x128 and
+  // 74 us with 256x128; k/v at M = 2048 21.9 -> 15.3 us with 64x64 instead of
+  // 128x128; q/o at M = 2048 (128 tiles of 256x256) keep 256x128 (39 vs 49 us).
   const int64_t cus = cu_count;
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-  if (t256 >= 2 * cus) return PrefillTile{256, 256, 2, 4, 64, 4, 4, true};
+  if (t256 * 8 >= cus * 5) return PrefillTile{256, 256, 2, 4, 64, 4, 4, true};
   const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
   if (t256x128 == cus || t256x128 >= 2 * cus) return PrefillTile{256, 128, 2, 4, 128, 3, 4};
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
@@ -807,6 +809,7 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
 #ifdef JV_PREFILL_ALL_TILES
     JV_PREFILL_PP_CASE(256, 256, 3)
     JV_PREFILL_PP_CASE(256, 128, 4)
+    JV_PREFILL_PP_CASE(256, 128, 3)
 #endif
 #undef JV_PREFILL_PP_CASE
     return hipErrorInvalidValue;
