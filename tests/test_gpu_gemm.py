@@ -293,6 +293,21 @@ def test_packed_activation_codes_prefill(M, N, K):
     check(y_packed[rows], x[rows], wq, sw)
 
 
+# Short K on every prefill form: the ping-pong 256x256 tile (M = 2048, N = 5120
+# gives 160 tiles), 256x128, 128x128 and 64x64, including K = 128 (two 64-deep
+# steps: the pipelines' shortest case) and a partial last token tile.
+@pytest.mark.parametrize("K", [128, 256, 384])
+@pytest.mark.parametrize("M,N", [(2048, 5120), (2000, 4096), (1024, 2048), (300, 1040)])
+def test_prefill_short_k(M, N, K):
+    x = synthetic.activations_heavy_tail(M, K, 150 + K).cuda()
+    wq, sw = quantize_rows(synthetic.weight(N, K, 151).cuda())
+    y = fp8_matmul(x, wq, sw)
+    if N % 16 == 0:
+        assert torch.equal(y, fp8_matmul(x, tile_weight(wq), sw, tiled=True))
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(K))[:64].sort().values.cuda()
+    check(y[rows], x[rows], wq, sw)
+
+
 @pytest.mark.parametrize("M", [1, 16, 40])
 def test_swiglu_packed_codes_feed_down_projection(M):
     I, N = 4096, 1024
