@@ -134,16 +134,23 @@ def quantized_operands(torch, fp8, x):
 def kernel_ms(b: Bench, fp8, rot, operands, name: str, replays: int) -> float:
     """Average time (ms) of one GEMM kernel launch for projection `name` on the
     activation codes fp8_matmul would produce, from graphs of back-to-back
-    launches on the bench stream."""
+    launches on the bench stream. The launches rotate over copies of this
+    projection's weights totalling at least ROTATE_BYTES, so each launch reads
+    its weights from HBM rather than the Infinity Cache."""
     xq, sx, packed_rows = operands
+    wq0, sw0 = rot[0][name]
+    n_copies = max(2, -(-ROTATE_BYTES // wq0.numel()) + 1)
+    copies = [(wq0, sw0)] + [(wq0.clone(), sw0) for _ in range(n_copies - 1)]
     graphs = []
-    for c in range(len(rot)):
+    for c in range(min(len(copies), 4)):
         def launches(c=c):
             for j in range(LAUNCHES_PER_GRAPH):
-                wq, sw = rot[(c + j) % len(rot)][name]
+                wq, sw = copies[(c * LAUNCHES_PER_GRAPH + j) % len(copies)]
                 fp8.fp8_matmul_quantized(xq, sx, wq, sw, packed_rows=packed_rows, tiled=True)
         graphs.append(b.capture(launches))
-    return b.time_graphs(graphs, replays, 3) / LAUNCHES_PER_GRAPH
+    ms = b.time_graphs(graphs, replays, 3) / LAUNCHES_PER_GRAPH
+    del graphs, copies
+    return ms
 
 
 def cpu_baseline(synthetic, M: int, budget_s: float) -> dict:
