@@ -308,7 +308,7 @@ def test_prefill_short_k(M, N, K):
     check(y[rows], x[rows], wq, sw)
 
 
-@pytest.mark.parametrize("M", [1, 16, 40])
+@pytest.mark.parametrize("M", [1, 16, 40, 300, 2048])
 def test_swiglu_packed_codes_feed_down_projection(M):
     I, N = 4096, 1024
     g = torch.Generator().manual_seed(130 + M)

@@ -59,6 +59,35 @@ def test_every_row_length(K):
     assert_matches_oracle(x, codes, scales)
 
 
+# Packed codes of prefill batches (the tile-per-workgroup kernel): every row
+# length class, special rows (huge, zero, inf, NaN, tiny) spread over the
+# tiles, a partial last tile.
+@pytest.mark.parametrize("K", [128, 1024, 2048, 4096, 6144, 12288, 16384])
+@pytest.mark.parametrize("M", [65, 200])
+def test_packed_prefill_rows(M, K):
+    from jeeves_amd.fp8 import packed_codes_bytes, tile_weight
+
+    g = torch.Generator().manual_seed(M * 7 + K)
+    x = torch.randn(M, K, generator=g) * torch.logspace(-12, 12, M)[:, None]
+    x[0, K // 3] = 5e4
+    x[17, :] = 0
+    x[33, 5] = float("inf")
+    x[50, 7] = float("nan")
+    x = x.to(torch.bfloat16).cuda()
+    want_codes, want_scales = quantize_rows(x)
+    assert_matches_oracle(x, want_codes, want_scales)
+    padded = torch.zeros((M + 15) // 16 * 16, K, dtype=torch.uint8, device="cuda")
+    padded[:M] = want_codes.view(torch.uint8)
+    want = tile_weight(padded).view(torch.uint8).reshape(-1)
+    packed = torch.full((packed_codes_bytes(M, K),), 0xAA, dtype=torch.uint8, device="cuda")
+    scales = torch.full((M,), float("nan"), device="cuda")
+    _lib.check(_lib.lib().jv_fp8_quantize_rows_bf16(x.data_ptr(), K, M, K, packed.data_ptr(), 0, scales.data_ptr(),
+                                                    helpers.stream()))
+    assert helpers.same_f32(scales.cpu().numpy(), want_scales.cpu().numpy()).all()
+    same = helpers.same_codes(packed.cpu().numpy(), want.cpu().numpy())
+    assert same.all(), f"{(~same).sum()} packed codes differ"
+
+
 def test_workload_activations():
     cases = [synthetic.single_linear()[0]]
     cases += [synthetic.decode_case(n, M)[0] for n in ("q", "down") for M in synthetic.DECODE_ROWS]
