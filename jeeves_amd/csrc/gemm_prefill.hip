@@ -86,10 +86,63 @@ __device__ __forceinline__ int64_t tiled_stage_offset(int kt) {
   return BK == 128 ? (int64_t)kt * 2048 : (int64_t)(kt >> 1) * 2048 + (kt & 1) * 512;
 }
 
+// LoRA operands of one wave's prefill tile (rank 16), loaded once at the
+// start of the epilogue: for block column j the B rows of channels
+// nb_j + l%32 (ranks 8h .. 8h+7, h = l/32: 8 bf16), for block row i the t
+// rows of tokens mb_i + l%32 (the same 8 ranks, fp32). Loads are clamped to
+// the last row; clamped outputs are never stored.
+template <int TN, int TM>
+struct LoraOperands {
+  i32x4 b[TN];
+  float4 t[TM][2];
+};
+
+template <int TN, int TM>
+__device__ __forceinline__ void load_lora(LoraOperands<TN, TM>& o, const Epilogue& ep, int nb, int mb, int M, int N,
+                                          int lane) {
+  const int h = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = min(nb + j * 32 + (lane & 31), N - 1);
+    o.b[j] = *reinterpret_cast<const i32x4*>(ep.lora_b + (int64_t)n * 16 + 8 * h);
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = min(mb + i * 32 + (lane & 31), M - 1);
+    const float4* t = reinterpret_cast<const float4*>(ep.lora_t + (int64_t)m * 16 + 8 * h);
+    o.t[i][0] = t[0];
+    o.t[i][1] = t[1];
+  }
+}
+
+// LoRA term of block (j, i): l[n, m] = sum_r B[n, r] t[m, r] in the fp8
+// blocks' accumulator layout, by two v_mfma_f32_32x32x16_bf16: t is split
+// into t_hi = bf16(t) and t_lo = bf16(t - t_hi) (about 16 significant bits),
+// the products with the bf16 B entries are exact, the sums fp32.
+__device__ __forceinline__ f32x16 lora_block(i32x4 b, const float4 (&t)[2]) {
+  const float tv[8] = {t[0].x, t[0].y, t[0].z, t[0].w, t[1].x, t[1].y, t[1].z, t[1].w};
+  uint32_t hi[4], lo[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    hi[e] = pack_bf16x2(tv[2 * e], tv[2 * e + 1]);
+    lo[e] = pack_bf16x2(tv[2 * e] - bf16_to_f32(hi[e] & 0xFFFFu), tv[2 * e + 1] - bf16_to_f32(hi[e] >> 16));
+  }
+  const bf16x8 bb = __builtin_bit_cast(bf16x8, b);
+  f32x16 l;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) l[r] = 0.0f;
+  l = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bb, __builtin_bit_cast(bf16x8, i32x4{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]}),
+                                              l, 0, 0, 0);
+  l = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bb, __builtin_bit_cast(bf16x8, i32x4{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]}),
+                                              l, 0, 0, 0);
+  return l;
+}
+
 // Epilogue of both FP8 prefill kernels. 32x32 MFMA output layout: lane l
 // holds column l % 32 (a token) and, in register r, row 8*(r/4) + 4*(l/32) +
 // r%4 (a channel): each register quad is 4 consecutive channels of one token.
-// The finished bf16 tile goes through LDS ([BM tokens][BN channels], 16-byte
+// y = bf16((acc * sx[m]) * sw[n] (+ bias[n]) (+ lora_scale * l[n, m])). The
+// finished bf16 tile goes through LDS ([BM tokens][BN channels], 16-byte
 // chunk c of row r stored at chunk c ^ (r % OUT_CH)) so that global stores are
 // 16 bytes per lane over whole row segments. The caller's operand reads and
 // copies into `lds` are complete (this wave's) when it is called.
@@ -102,6 +155,9 @@ __device__ __forceinline__ void store_tile(uint8_t* lds, const float* scale_lds,
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int OUT_CH = BN * 2 / 16;  // 16-byte chunks per output tile row
   static_assert(OUT_CH <= 32 && (OUT_CH & (OUT_CH - 1)) == 0, "output tile width");
+  static_assert(RANK == 0 || RANK == 16, "LoRA rank");
+  LoraOperands<TN, TM> lo;
+  if constexpr (RANK > 0) load_lora(lo, ep, n0 + wn * WN, m0 + wm * WM, M, N, lane);
   float sxm[TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i) sxm[i] = scale_lds[wm * WM + i * 32 + (lane & 31)];
@@ -110,19 +166,23 @@ __device__ __forceinline__ void store_tile(uint8_t* lds, const float* scale_lds,
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int nl = wn * WN + j * 32 + 8 * q + 4 * (lane >> 5);  // channel within the tile
-      const int n = n0 + nl;
-      const float4 swq = *reinterpret_cast<const float4*>(scale_lds + BM + nl);
-      const float sw4[4] = {swq.x, swq.y, swq.z, swq.w};
+    for (int i = 0; i < TM; ++i) {
+      const int ml = wm * WM + i * 32 + (lane & 31);  // token within the tile
+      const int m = min(m0 + ml, M - 1);
+      f32x16 lora;
+      if constexpr (RANK > 0) lora = lora_block(lo.b[j], lo.t[i]);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int ml = wm * WM + i * 32 + (lane & 31);  // token within the tile
-        const int m = min(m0 + ml, M - 1);
+      for (int q = 0; q < 4; ++q) {
+        const int nl = wn * WN + j * 32 + 8 * q + 4 * (lane >> 5);  // channel within the tile
+        const int n = n0 + nl;
+        const float4 swq = *reinterpret_cast<const float4*>(scale_lds + BM + nl);
+        const float sw4[4] = {swq.x, swq.y, swq.z, swq.w};
         float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          v[e] = epilogue_value<RANK>(ep, acc[j][i][4 * q + e], m, min(n + e, N - 1), sxm[i], sw4[e]);
+        for (int e = 0; e < 4; ++e) {
+          v[e] = epilogue_value<0>(ep, acc[j][i][4 * q + e], m, min(n + e, N - 1), sxm[i], sw4[e]);
+          if constexpr (RANK > 0) v[e] += lora[4 * q + e] * ep.lora_scale;
+        }
         const int chunk = (nl >> 3) ^ (ml % OUT_CH);
         *reinterpret_cast<uint2*>(lds + ml * (BN * 2) + chunk * 16 + (nl & 4) * 2) =
             uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
@@ -754,23 +814,28 @@ static hipError_t launch_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* 
   return hipGetLastError();
 }
 
-// The ping-pong form (no LoRA epilogue: with it the kernel needs more than
-// the 256 registers two waves per SIMD leave each wave).
 template <int BM, int BN, int STAGES>
 static hipError_t launch_prefill_pp(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
-                                    const Epilogue& ep, int group_m, hipStream_t stream) {
+                                    const Epilogue& ep, int rank, int group_m, hipStream_t stream) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
   const dim3 grid((unsigned)(tm * tn)), block(512);
   if (group_m < 1) group_m = 1;
-#define JV_PREFILL_PP_LAUNCH(PW, PX) \
-  gemm_prefill_pp_kernel<BM, BN, STAGES, 0, PW, PX><<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep)
-  if (ldw == 0) {
-    if (ldx == 0) JV_PREFILL_PP_LAUNCH(true, true);
-    else JV_PREFILL_PP_LAUNCH(true, false);
-  } else {
-    if (ldx == 0) JV_PREFILL_PP_LAUNCH(false, true);
-    else JV_PREFILL_PP_LAUNCH(false, false);
+#define JV_PREFILL_PP_LAUNCH(R, PW, PX) \
+  gemm_prefill_pp_kernel<BM, BN, STAGES, R, PW, PX><<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep)
+#define JV_PREFILL_PP_LAUNCH_R(R)                          \
+  if (ldw == 0) {                                          \
+    if (ldx == 0) JV_PREFILL_PP_LAUNCH(R, true, true);     \
+    else JV_PREFILL_PP_LAUNCH(R, true, false);             \
+  } else {                                                 \
+    if (ldx == 0) JV_PREFILL_PP_LAUNCH(R, false, true);    \
+    else JV_PREFILL_PP_LAUNCH(R, false, false);            \
   }
+  if (rank == 16) {
+    JV_PREFILL_PP_LAUNCH_R(16)
+  } else {
+    JV_PREFILL_PP_LAUNCH_R(0)
+  }
+#undef JV_PREFILL_PP_LAUNCH_R
 #undef JV_PREFILL_PP_LAUNCH
   return hipGetLastError();
 }
@@ -800,11 +865,11 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
                         const Epilogue& ep, int rank, PrefillTile t, hipStream_t stream) {
   if (rank != 0 && rank != 16) return hipErrorInvalidValue;
   if (K % t.bk || K % 128) return hipErrorInvalidValue;
-  if (t.pingpong && rank == 0) {
+  if (t.pingpong) {
     if (t.wgm != 2 || t.wgn != 4 || t.bk != 64) return hipErrorInvalidValue;
 #define JV_PREFILL_PP_CASE(BM_, BN_, ST_) \
   if (t.bm == BM_ && t.bn == BN_ && t.stages == ST_) \
-    return launch_prefill_pp<BM_, BN_, ST_>(xq, ldx, w, ldw, M, N, K, ep, t.group_m, stream);
+    return launch_prefill_pp<BM_, BN_, ST_>(xq, ldx, w, ldw, M, N, K, ep, rank, t.group_m, stream);
     JV_PREFILL_PP_CASE(256, 256, 4)
 #ifdef JV_PREFILL_ALL_TILES
     JV_PREFILL_PP_CASE(256, 256, 3)
@@ -814,9 +879,6 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
 #undef JV_PREFILL_PP_CASE
     return hipErrorInvalidValue;
   }
-  // With a LoRA epilogue the 256x256 tile needs more registers than two waves
-  // per SIMD leave each wave: such launches take 256x128 tiles.
-  if (t.pingpong || (rank == 16 && t.bm == 256 && t.bn == 256)) t = PrefillTile{256, 128, 2, 4, 128, 3, 4};
 #define JV_PREFILL_CASE(BM_, BN_, WGM_, WGN_, BK_, ST_)                                                     \
   if (t.bm == BM_ && t.bn == BN_ && t.wgm == WGM_ && t.wgn == WGN_ && t.bk == BK_ && t.stages == ST_)       \
     return launch_prefill<BM_, BN_, WGM_, WGN_, BK_, ST_>(xq, ldx, w, ldw, M, N, K, ep, rank, t.group_m, stream);

@@ -167,6 +167,25 @@ def test_bias_and_lora_epilogue():
         check(y, x, wq, sw, bias=bias, lora=(a, b, synthetic.LORA_SCALING))
 
 
+@pytest.mark.parametrize("M,N", [(2048, 24576), (1000, 5120)])
+def test_lora_prefill_on_every_tile_form(M, N):
+    """Bias + LoRA on the ping-pong 256x256 tiles (the LoRA term of each 32x32
+    block by fp32 MFMAs in the epilogue) against the oracle on sampled rows,
+    and row slices that land on the lockstep tile forms give the same bits."""
+    K = 4096
+    x = synthetic.activations_heavy_tail(M, K, 160 + M).cuda()
+    wq, sw = quantize_rows(synthetic.weight(N, K, 161).cuda())
+    a, b = synthetic.lora_factors(N, K, 162)
+    a, b = a.cuda(), b.cuda()
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(3)) * 0.1).to(torch.bfloat16).cuda()
+    lora = (a, b, synthetic.LORA_SCALING)
+    y = fp8_matmul(x, wq, sw, bias=bias, lora=lora)
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(4))[:32].sort().values.cuda()
+    check(y[rows], x[rows], wq, sw, bias=bias, lora=lora)
+    for lo, hi in ((0, 300), (M - 129, M)):
+        assert torch.equal(y[lo:hi], fp8_matmul(x[lo:hi].contiguous(), wq, sw, bias=bias, lora=lora)), (lo, hi)
+
+
 def test_every_code_decodes_through_both_kernels():
     # check_kernel_on_every_code (inference/fp8_metal.py:38-46): identity
     # activations pick every finite code of a permuted weight table.
