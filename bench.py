@@ -18,6 +18,11 @@ roofline     the dominant kernel (the fused gate+up decode GEMM) alone: a graph
              on its stream; algorithmic bytes / average launch time vs 8 TB/s
 prefill      the same six projections at M = 2048 (TFLOP/s, 2*M*N*K per
              linear), with the gate+up prefill GEMM's roofline vs 5.0 PFLOP/s
+workloads    the decoder layer's linear stack at M = 512 with a rank-16 LoRA
+             on every projection, and the ragged request mix (64 log-uniform
+             sequence lengths packed into one batch through 32 layers of
+             random weights, then 64 decode steps at batch 64): time,
+             TFLOP/s or GB/s and roofline fraction per phase
 cpu_baseline the CPU oracle's dequantize-then-matmul (numpy float32, BLAS
              threads) on the same decode step, timed on the host for a bounded
              number of steps
@@ -206,6 +211,120 @@ def pmc_driver(torch, fp8, synthetic, quantize_rows, launches: int = 10) -> None
     print("pmc driver done", flush=True)
 
 
+def device_weight(torch, synthetic, N: int, K: int, seed: int):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return (torch.randn(N, K, device="cuda", generator=g) * synthetic.WEIGHT_STD).to(torch.bfloat16)
+
+
+def layer_linears(fp8, synthetic, h, weights, lora=None):
+    """One decoder layer's linear stack on h: q, k, v, o and gate+up, SwiGLU
+    fused with the down projection's activation quantization, down (the same
+    input feeds every projection: only the linear layers are timed)."""
+    for name in ("q", "k", "v", "o"):
+        wq, sw = weights[name]
+        fp8.fp8_matmul(h, wq, sw, tiled=True, lora=lora[name] if lora else None)
+    wq, sw = weights["gate_up"]
+    gu = fp8.fp8_matmul(h, wq, sw, tiled=True, lora=lora["gate_up"] if lora else None)
+    inter = synthetic.INTERMEDIATE
+    res = fp8.swiglu_quantize(gu[:, :inter], gu[:, inter:], lora_a=lora["down"][0] if lora else None, packed=True)
+    wq, sw = weights["down"]
+    return fp8.fp8_matmul_quantized(res[0], res[1], wq, sw, lora_t=res[2] if lora else None,
+                                    lora_b=lora["down"][1] if lora else None,
+                                    lora_scaling=lora["down"][2] if lora else 0.0, packed_rows=h.shape[0], tiled=True)
+
+
+def layer_flops(synthetic, M: int, rank: int = 0) -> int:
+    return sum(2 * M * N * K + 2 * M * rank * (K + N) for N, K in synthetic.SHAPES.values())
+
+
+def workloads(torch, b: Bench, fp8, synthetic, quantize_rows) -> dict:
+    """The decoder layer with LoRA at M = 512 and the ragged request mix through
+    32 layers (prefill of the packed batch, then 64 decode steps at batch 64):
+    linear-layer time, throughput and roofline fraction of each phase."""
+    out = {}
+    # decoder layer, M = 512, rank-16 LoRA on every projection; 4 weight copies (772 MB) rotate
+    M = 512
+    x = synthetic.activations_heavy_tail(M, synthetic.HIDDEN, 400).cuda()
+    copies, lora = [], {}
+    for c in range(4):
+        weights = {}
+        for i, (name, (N, K)) in enumerate(synthetic.SHAPES.items()):
+            wq, sw = quantize_rows(device_weight(torch, synthetic, N, K, 410 + i + 10 * c))
+            weights[name] = (fp8.tile_weight(wq), sw)
+            if c == 0:
+                a, bb = synthetic.lora_factors(N, K, 420 + i)
+                lora[name] = (a.cuda(), bb.cuda(), synthetic.LORA_SCALING)
+        copies.append(weights)
+    graphs = [b.capture(lambda c=c: layer_linears(fp8, synthetic, x, copies[c], lora)) for c in range(len(copies))]
+    ms = b.time_graphs(graphs, 40, 4)
+    fl = layer_flops(synthetic, M, synthetic.LORA_RANK)
+    tf = fl / (ms * 1e-3) / 1e12
+    out["decoder_layer_lora_m512"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
+                                      "flops": fl, "note": "q, k, v, o, gate+up, SwiGLU-quant, down with rank-16 LoRA each; "
+                                                           "HIP graph replay over 4 weight copies (772 MB)"}
+    del graphs, copies
+    torch.cuda.empty_cache()
+    log(f"bench: decoder layer (LoRA, M=512) {ms * 1e3:.1f} us, {tf:.0f} TFLOP/s")
+
+    # ragged mix: 32 layers of random weights (6.2 GB of e4m3 codes)
+    layers = []
+    for layer in range(32):
+        weights = {}
+        for i, (name, (N, K)) in enumerate(synthetic.SHAPES.items()):
+            wq, sw = quantize_rows(device_weight(torch, synthetic, N, K, 700 + 10 * layer + i))
+            weights[name] = (fp8.tile_weight(wq), sw)
+        layers.append(weights)
+    torch.cuda.empty_cache()
+    lengths = synthetic.ragged_lengths()
+    h = torch.cat([synthetic.activations_heavy_tail(n, synthetic.HIDDEN, 5000 + i) for i, n in enumerate(lengths)]).cuda()
+    T = h.shape[0]
+    with torch.cuda.stream(b.stream):
+        for weights in layers[:2]:
+            layer_linears(fp8, synthetic, h, weights)
+        b.stream.synchronize()
+        best = None
+        for _ in range(2):
+            st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            st.record(b.stream)
+            for weights in layers:
+                layer_linears(fp8, synthetic, h, weights)
+            en.record(b.stream)
+            en.synchronize()
+            t = st.elapsed_time(en)
+            best = t if best is None else min(best, t)
+    pre_ms = best
+    pre_fl = 32 * layer_flops(synthetic, T)
+    pre_tf = pre_fl / (pre_ms * 1e-3) / 1e12
+    del h
+    torch.cuda.empty_cache()
+    xd = synthetic.activations_outliers(64, synthetic.HIDDEN, 5500).cuda()
+
+    def decode_step():
+        for weights in layers:
+            layer_linears(fp8, synthetic, xd, weights)
+
+    g = b.capture(decode_step)
+    step_ms = b.time_graphs([g], 64, 2)
+    dec_bytes = 32 * sum(linear_bytes(64, N, K) for N, K in synthetic.SHAPES.values())
+    dec_gbs = dec_bytes / (step_ms * 1e-3) / 1e9
+    out["ragged_32_layers"] = {
+        "tokens_prefill": T, "sequences": len(lengths),
+        "prefill_ms": round(pre_ms, 3), "prefill_TFLOP/s": round(pre_tf, 1),
+        "prefill_frac_of_fp8_peak": round(pre_tf / FP8_PEAK_TFLOPS, 4),
+        "decode_steps": 64, "decode_batch": 64, "decode_ms_total": round(64 * step_ms, 3),
+        "decode_us_per_step": round(step_ms * 1e3, 1), "decode_GB/s": round(dec_gbs, 1),
+        "decode_frac_of_hbm_peak": round(dec_gbs / HBM_PEAK_GBS, 4),
+        "linear_ms_total": round(pre_ms + 64 * step_ms, 3),
+        "note": "linear layers only (q, k, v, o, gate+up, SwiGLU-quant, down per layer, no LoRA), random-init "
+                "weights; prefill eager on the packed batch, each decode step one HIP graph of 32 layers",
+    }
+    log(f"bench: ragged prefill {T} tokens {pre_ms:.2f} ms ({pre_tf:.0f} TFLOP/s), decode step {step_ms * 1e3:.0f} us "
+        f"({dec_gbs:.0f} GB/s)")
+    del g, layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -216,6 +335,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="skip the decoder-layer (LoRA, M=512) and 32-layer ragged-mix measurements")
     ap.add_argument("--pmc-driver", action="store_true",
                     help="run only the hardware-counter workload (copy calibration + gate+up GEMMs), no timing")
     args = ap.parse_args()
@@ -321,6 +442,9 @@ def main() -> int:
             "kernels": pshape,
         }
         log(f"bench: prefill step {pms:.3f} ms, kernels {pshape}")
+
+    if not args.no_workloads:
+        result["workloads"] = workloads(torch, b, fp8, synthetic, quantize_rows)
 
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")
