@@ -19,10 +19,11 @@ roofline     the dominant kernel (the fused gate+up decode GEMM) alone: a graph
 prefill      the same six projections at M = 2048 (TFLOP/s, 2*M*N*K per
              linear), with the gate+up prefill GEMM's roofline vs 5.0 PFLOP/s
 workloads    the decoder layer's linear stack at M = 512 with a rank-16 LoRA
-             on every projection, and the ragged request mix (64 log-uniform
+             on every projection, the ragged request mix (64 log-uniform
              sequence lengths packed into one batch through 32 layers of
-             random weights, then 64 decode steps at batch 64): time,
-             TFLOP/s or GB/s and roofline fraction per phase
+             random weights, then 64 decode steps at batch 64), and the
+             lm_head (248320 x 4096) at M = 1 and 16: time, TFLOP/s or GB/s
+             and roofline fraction per phase
 cpu_baseline the CPU oracle's dequantize-then-matmul (numpy float32, BLAS
              threads) on the same decode step, timed on the host for a bounded
              number of steps
@@ -321,6 +322,26 @@ def workloads(torch, b: Bench, fp8, synthetic, quantize_rows) -> dict:
     log(f"bench: ragged prefill {T} tokens {pre_ms:.2f} ms ({pre_tf:.0f} TFLOP/s), decode step {step_ms * 1e3:.0f} us "
         f"({dec_gbs:.0f} GB/s)")
     del g, layers
+    torch.cuda.empty_cache()
+
+    # lm_head, N = 248320 x K = 4096 (inference/engine.py:293-297): 1.02 GB of tiled e4m3 codes, more
+    # than the rotation size, so every call reads its weights from HBM; quantizer + GEMM per call
+    N, K = synthetic.VOCAB, synthetic.HIDDEN
+    wq, sw = quantize_rows(device_weight(torch, synthetic, N, K, 600))
+    wq = fp8.tile_weight(wq)
+    torch.cuda.empty_cache()
+    heads = {}
+    for M in (1, 16):
+        x = synthetic.activations_outliers(M, K, 610 + M).cuda()
+        g = b.capture(lambda x=x: [fp8.fp8_matmul(x, wq, sw, tiled=True) for _ in range(4)])
+        ms = b.time_graphs([g], 10, 2) / 4
+        gbs = linear_bytes(M, N, K) / (ms * 1e-3) / 1e9
+        heads[f"m{M}"] = {"us": round(ms * 1e3, 1), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        del g
+    out["lm_head_decode"] = dict(heads, note="N=248320 K=4096 (1.02 GB e4m3, tiled), per-token quantizer + GEMM per "
+                                             "call, HIP graph of 4 calls")
+    log(f"bench: lm_head decode {heads}")
+    del wq, sw
     torch.cuda.empty_cache()
     return out
 

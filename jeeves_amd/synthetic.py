@@ -38,6 +38,8 @@ SHAPES: dict[str, tuple[int, int]] = {
     "down": (HIDDEN, INTERMEDIATE),
 }
 SHAPE_INDEX = {name: i for i, name in enumerate(SHAPES)}
+# lm_head (inference/engine.py:293-297): the 9B vocabulary x hidden, 1.02 GB of e4m3 codes.
+VOCAB = 248320
 DECODE_ROWS = (1, 4, 16, 32)
 PREFILL_ROWS = (512, 2048, 8192)
 LORA_RANK, LORA_ALPHA = 16, 32.0

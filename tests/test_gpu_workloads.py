@@ -42,7 +42,7 @@ def device_weight(N, K, seed):
 
 @pytest.fixture(scope="module")
 def lm_head():
-    w = device_weight(248320, 4096, 600)
+    w = device_weight(synthetic.VOCAB, synthetic.HIDDEN, 600)
     wq, sw = quantize_rows(w)
     del w
     torch.cuda.empty_cache()
@@ -56,8 +56,8 @@ def test_lm_head_vocab_logits(lm_head, M):
     wq, sw = lm_head
     x = synthetic.activations_outliers(M, 4096, 610 + M).cuda()
     y = fp8_matmul(x, wq, sw)
-    assert y.shape == (M, 248320)
-    cols = torch.randperm(248320, generator=torch.Generator().manual_seed(M))[:2048].sort().values.cuda()
+    assert y.shape == (M, synthetic.VOCAB)
+    cols = torch.randperm(synthetic.VOCAB, generator=torch.Generator().manual_seed(M))[:2048].sort().values.cuda()
     check_rows(y, x, wq, sw, cols=cols)
     assert torch.equal(y[:, -16:], fp8_matmul(x, wq[-16:], sw[-16:])) if M > 64 else True
     assert torch.equal(y, fp8_matmul(x, wq, sw))
