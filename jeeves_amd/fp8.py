@@ -82,6 +82,25 @@ def _check_weight(K: int, weight: torch.Tensor) -> None:
                          f"of shape {tuple(weight.shape)}")
 
 
+def _check_operands(dev: torch.device, N: int, weight: torch.Tensor, scale: torch.Tensor,
+                    bias: torch.Tensor | None = None, *others: torch.Tensor | None) -> None:
+    """Every operand on the activations' HIP device (a host or foreign-device
+    pointer in a kernel argument is a GPU memory fault, not an error; the
+    reference's Triton launcher rejects such tensors with a ValueError too),
+    one-byte weight codes, and one scale (and bias) per output channel."""
+    if dev.type != "cuda":
+        raise ValueError(f"the fp8 GEMM runs on a HIP device; the activations are on {dev}")
+    if weight.element_size() != 1:
+        raise ValueError(f"weight codes must be float8_e4m3fn (or uint8), got {weight.dtype}")
+    if scale.numel() != N:
+        raise ValueError(f"scale needs one value per output channel ({N}), got {scale.numel()}")
+    if bias is not None and bias.numel() != N:
+        raise ValueError(f"bias needs one value per output channel ({N}), got {bias.numel()}")
+    for t in (weight, scale, bias, *others):
+        if t is not None and t.device != dev:
+            raise ValueError(f"the fp8 GEMM's operands must all be on {dev}, got one on {t.device}")
+
+
 def _weight_operand(weight: torch.Tensor, tiled: bool) -> tuple[torch.Tensor, int]:
     """Weight bytes and the C ABI's ldw: the row stride, or 0 for the tiled
     layout (``tile_weight``)."""
@@ -164,6 +183,7 @@ def fp8_matmul(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *, bi
     _check_weight(K, weight)
     a, b, rank, scaling = _check_lora(lora, K, N)
     dev = x.device
+    _check_operands(dev, N, weight, scale, bias, a, b)
     if x.dtype != torch.bfloat16:
         x = x.to(torch.bfloat16)
     if not _rows_aligned(x, 2):
@@ -204,6 +224,7 @@ def fp8_matmul_w8a16(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
     N = weight.shape[0]
     _check_weight(K, weight)
     dev = x.device
+    _check_operands(dev, N, weight, scale, bias)
     if x.dtype != torch.bfloat16:
         x = x.to(torch.bfloat16)
     if not _rows_aligned(x, 2):
@@ -257,9 +278,14 @@ def fp8_matmul_quantized(xq: torch.Tensor, x_scale: torch.Tensor, weight: torch.
         M, K = xq.shape
     _check_weight(K, weight)
     rank = 0 if lora_t is None else lora_t.shape[1]
-    if rank and (rank not in LORA_RANKS or lora_b is None or lora_b.shape != (N, rank)):
-        raise ValueError("lora_t needs lora_b [N, r] with r in (16,)")
+    if rank and (rank not in LORA_RANKS or lora_b is None or lora_b.shape != (N, rank) or lora_t.shape != (M, rank)):
+        raise ValueError(f"lora_t [M, r] needs lora_b [N, r] with r in {LORA_RANKS}")
     dev = xq.device
+    if xq.element_size() != 1:
+        raise ValueError(f"activation codes must be float8_e4m3fn (or uint8), got {xq.dtype}")
+    if x_scale.numel() != M:
+        raise ValueError(f"x_scale needs one value per token row ({M}), got {x_scale.numel()}")
+    _check_operands(dev, N, weight, scale, bias, x_scale, lora_t, lora_b)
     xq = xq.view(torch.uint8)
     if packed_rows is None and not _rows_aligned(xq, 1):
         xq = xq.contiguous()
@@ -299,6 +325,8 @@ def swiglu_quantize(gate: torch.Tensor, up: torch.Tensor, *, lora_a: torch.Tenso
     if up.shape != gate.shape:
         raise ValueError(f"gate {tuple(gate.shape)} and up {tuple(up.shape)} differ")
     dev = gate.device
+    if dev.type != "cuda" or up.device != dev or (lora_a is not None and lora_a.device != dev):
+        raise ValueError(f"swiglu_quantize needs gate, up and lora_a on one HIP device, got {dev} and {up.device}")
     gate, up = gate.to(torch.bfloat16), up.to(torch.bfloat16)
     if not _rows_aligned(gate, 2):
         gate = gate.contiguous()

@@ -231,6 +231,35 @@ def test_row_strided_input_and_zero_rows():
     assert not zeros.float().abs().sum().item()
 
 
+def test_operands_on_another_device_or_of_the_wrong_size_are_refused():
+    """Weights, scales, biases and LoRA factors left on the host (their
+    pointers would fault the GPU) and per-channel vectors of the wrong length
+    raise ValueError before any launch; the stream stays usable."""
+    from jeeves_amd.fp8 import fp8_matmul_w8a16
+
+    M, N, K = 16, 1024, 4096
+    x = synthetic.activations_heavy_tail(M, K, 130).cuda()
+    wq, sw = quantize_rows(synthetic.weight(N, K, 131).cuda())
+    bias = torch.zeros(N, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="operands must all be on"):
+        fp8_matmul(x, wq.cpu(), sw)
+    with pytest.raises(ValueError, match="operands must all be on"):
+        fp8_matmul(x, wq, sw.cpu())
+    with pytest.raises(ValueError, match="operands must all be on"):
+        fp8_matmul(x, wq, sw, bias=bias.cpu())
+    with pytest.raises(ValueError, match="operands must all be on"):
+        fp8_matmul(x, wq, sw, lora=(torch.zeros(16, K), torch.zeros(N, 16), 2.0))
+    with pytest.raises(ValueError, match="operands must all be on"):
+        fp8_matmul_w8a16(x, wq.cpu(), sw)
+    with pytest.raises(ValueError, match="one value per output channel"):
+        fp8_matmul(x, wq, sw[: N - 1])
+    with pytest.raises(ValueError, match="one value per output channel"):
+        fp8_matmul(x, wq, sw, bias=bias[:16])
+    with pytest.raises(ValueError, match="weight codes"):
+        fp8_matmul(x, wq.to(torch.bfloat16), sw)
+    check(fp8_matmul(x, wq, sw), x, wq, sw)
+
+
 def test_graph_capture_and_replay():
     """Both kernels under HIP graph capture: replays after new inputs match eager
     calls (the split-K counters are created outside the capture)."""

@@ -103,6 +103,29 @@ def test_fp8_matmul_validates_before_launch():
         fp8_matmul(x, w, torch.ones(64), lora=(torch.zeros(8, 256), torch.zeros(64, 8), 2.0))
 
 
+def test_operands_must_sit_on_a_hip_device():
+    """A host pointer passed to a kernel is a GPU memory fault, so host tensors
+    are refused before anything is enqueued (as the reference's Triton
+    launcher refuses them), and so are weights that are not one-byte codes and
+    scales or biases of the wrong length."""
+    from jeeves_amd.fp8 import fp8_matmul_quantized, fp8_matmul_w8a16, swiglu_quantize
+
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    w = torch.zeros(64, 256, dtype=torch.uint8).view(FP8)
+    with pytest.raises(ValueError, match="HIP device"):
+        fp8_matmul(x, w, torch.ones(64))
+    with pytest.raises(ValueError, match="HIP device"):
+        fp8_matmul_w8a16(x, w, torch.ones(64))
+    with pytest.raises(ValueError, match="HIP device"):
+        fp8_matmul_quantized(torch.zeros(4, 256, dtype=torch.uint8), torch.ones(4), w, torch.ones(64))
+    with pytest.raises(ValueError, match="HIP device"):
+        swiglu_quantize(torch.zeros(4, 256, dtype=torch.bfloat16), torch.zeros(4, 256, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="x_scale"):
+        fp8_matmul_quantized(torch.zeros(4, 256, dtype=torch.uint8), torch.ones(3), w, torch.ones(64))
+    with pytest.raises(ValueError, match="activation codes"):
+        fp8_matmul_quantized(torch.zeros(4, 256, dtype=torch.bfloat16), torch.ones(4), w, torch.ones(64))
+
+
 def test_set_lora_validates_shapes():
     m = FP8Linear(256, 1024, device="meta")
     with pytest.raises(ValueError):
