@@ -55,7 +55,7 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K) {
 
 // Bytes of the split-K partials for these sizes (0 when no split).
 int64_t partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
-  if (M > jv::kDecodeMaxRows) return 0;
+  if (!jv::decode_kernel_for(M, N, cus)) return 0;
   const int s = jv::decode_plan(M, N, K, cus).splits;
   return s > 1 ? round_up((int64_t)s * M * N * 4, 256) : 0;
 }
@@ -74,7 +74,7 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, co
   if ((uint64_t)M * (uint64_t)ldxq >= (1ull << 32) || (uint64_t)jv::packed_x_bytes(M, K) >= (1ull << 32))
     return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
   jv::Epilogue ep{sx, sw, bias, lora_t, lora_b, lora_scaling, y, ldy};
-  if (M <= jv::kDecodeMaxRows) {
+  if (jv::decode_kernel_for(M, N, cus)) {
     const jv::DecodePlan plan = jv::decode_plan(M, N, K, cus);
     const int splits = plan.splits;
     float* partial = nullptr;
@@ -292,12 +292,12 @@ int jv_fp8_untile_weight(const void* tiled, int64_t N, int64_t K, void* codes, i
 }
 
 int jv_fp8_split_for(int64_t M, int64_t N, int64_t K, int cu_count) {
-  if (M > jv::kDecodeMaxRows || K <= 0 || N <= 0 || cu_count <= 0) return 1;
+  if (K <= 0 || N <= 0 || cu_count <= 0 || !jv::decode_kernel_for(M, N, cu_count)) return 1;
   return jv::decode_plan(M, N, K, cu_count).splits;
 }
 
 int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count) {
-  if (M > jv::kDecodeMaxRows || K <= 0 || N <= 0 || cu_count <= 0) return 0;
+  if (K <= 0 || N <= 0 || cu_count <= 0 || !jv::decode_kernel_for(M, N, cu_count)) return 0;
   const jv::DecodePlan p = jv::decode_plan(M, N, K, cu_count);
   return p.splits > 1 ? p.groups : 0;
 }

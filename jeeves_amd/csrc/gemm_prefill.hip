@@ -851,6 +851,10 @@ PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count) {
   // at M = 512 (192 tiles of 256x256) 52.7 us against 72 us with 128x128 and
   // 74 us with 256x128; k/v at M = 2048 21.9 -> 15.3 us with 64x64 instead of
   // 128x128; q/o at M = 2048 (128 tiles of 256x256) keep 256x128 (39 vs 49 us).
+  // Batches of at most 64 tokens that reach the prefill kernel (wide weights,
+  // decode_kernel_for) take 64x64 tiles: 23.4 us for gate+up at M = 64 vs
+  // 25.9 with 64x128 and 45.9 with 128x64.
+  if (M <= kDecodeMaxRows) return {64, 64, 2, 2, 128, 4, 8};
   const int64_t cus = cu_count;
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
   if (t256 * 8 >= cus * 5) return PrefillTile{256, 256, 2, 4, 64, 4, 4, true};

@@ -11,6 +11,19 @@ namespace jv {
 // Decode regime: M <= kDecodeMaxRows tokens.
 constexpr int kDecodeMaxRows = 64;
 
+// The decode kernel takes M <= 16 tokens, and up to kDecodeMaxRows tokens
+// unless the weight is wide enough for 1.5 rounds of 64-channel tiles of the
+// prefill kernel (measured on MI355X: gate+up, N = 24576, 23.4 vs 30.4 us at
+// M = 64, 23.1 vs 28.7 at M = 40, 21.6 vs 22.4 at M = 24; the lm_head,
+// N = 248320, 193 vs 236 us at M = 64 and 179 vs 202 at M = 32; q/o, k/v and
+// down stay on the decode kernel, 1.4-1.8x faster there). Those prefill
+// tiles stage each 16-token tile's codes in LDS once per workgroup, where
+// the decode waves each load every code fragment.
+inline bool decode_kernel_for(int64_t M, int64_t N, int cu_count) {
+  if (M > kDecodeMaxRows) return false;
+  return M <= 16 || 2 * ((N + 63) / 64) < 3 * (int64_t)cu_count;
+}
+
 struct DecodePlan {
   int rt;      // 16-row tiles per wave
   int waves;   // waves per workgroup, splitting the workgroup's k range

@@ -12,7 +12,9 @@ kernels of ``libjeeves_fp8.so``, called through its C ABI:
 * the GEMM multiplies e4m3 by e4m3 on the FP8 MFMA units and applies
   ``acc * sx[m] * sw[n]`` (+ bias, + optional LoRA) in its epilogue;
 * M <= ``DECODE_MAX_ROWS`` runs the HBM-bound split-K decode kernel, larger M
-  the LDS-tiled prefill kernel.
+  the LDS-tiled prefill kernel; batches of 17-64 tokens on weights wide enough
+  for 1.5 rounds of 64-channel tiles (gate+up, the lm_head) take the prefill
+  kernel's 64x64 tiles, which load each code fragment once per workgroup.
 
 Everything is enqueued on ``torch.cuda.current_stream()`` without host
 synchronisation; outputs and workspaces come from torch's caching allocator
@@ -29,7 +31,8 @@ from .device import sm_count
 from .fp8_weights import FP8, quantize_rows
 
 # Rows at or below which fp8_matmul takes the decode kernel (the role of
-# SPLIT_K_MAX_ROWS, inference/fp8.py:20): up to four 16-token MFMA column tiles.
+# SPLIT_K_MAX_ROWS, inference/fp8.py:20): up to four 16-token MFMA column tiles
+# (above 16 rows only on weights too narrow for 1.5 rounds of 64x64 prefill tiles).
 DECODE_MAX_ROWS = 64
 # Longest row the single-pass quantizer (and so the packed code layout) covers.
 QUANT_MAX_PACKED_COLS = 16384

@@ -91,6 +91,27 @@ def test_decode_workload_shapes(name, M):
         assert torch.equal(y, yq)
 
 
+@pytest.mark.parametrize("N", [24576, 24592])
+@pytest.mark.parametrize("M", [17, 24, 40, 64])
+def test_wide_small_batches_take_64x64_prefill_tiles(N, M):
+    """17-64 tokens on weights wide enough for 1.5 rounds of 64-channel
+    tiles (gate+up, the lm_head) run on the prefill kernel's 64x64 tiles:
+    oracle criteria, packed and row-major codes bitwise equal, row-major and
+    tiled weights bitwise equal, bias and LoRA in the same epilogue."""
+    K = 4096
+    x = synthetic.activations_heavy_tail(M, K, 140 + M).cuda()
+    wq, sw = quantize_rows(synthetic.weight(N, K, 141).cuda())
+    y = fp8_matmul(x, wq, sw)
+    check(y, x, wq, sw)
+    assert torch.equal(y, fp8_matmul(x, tile_weight(wq), sw, tiled=True))
+    xq, sx = quantize_rows(x)
+    assert torch.equal(y, fp8_matmul_quantized(xq, sx, wq, sw))
+    a, b = synthetic.lora_factors(N, K, 142)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(143)) * 0.1).to(torch.bfloat16).cuda()
+    lora = (a.cuda(), b.cuda(), synthetic.LORA_SCALING)
+    check(fp8_matmul(x, wq, sw, bias=bias, lora=lora), x, wq, sw, bias=bias, lora=lora)
+
+
 @pytest.mark.parametrize("N,K", [(256, 4096), (128, 12288), (144, 1024), (144, 2048)])
 @pytest.mark.parametrize("M", [1, 16, 33, 64])
 def test_split_k_decode_path(N, K, M):
