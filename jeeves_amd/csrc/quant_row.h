@@ -37,9 +37,10 @@ __device__ __forceinline__ uint32_t swiglu_pair(uint32_t g2, uint32_t u2) {
   return swiglu_bf16(g2 & 0xFFFFu, u2 & 0xFFFFu) | (swiglu_bf16(g2 >> 16, u2 >> 16) << 16);
 }
 
-template <int RANK>
-__device__ __forceinline__ void lora_accumulate(float (&t)[RANK > 0 ? RANK : 1], uint4 v, const uint16_t* __restrict__ a,
-                                                int64_t K, int c) {
+// t[r] += sum over the chunk's 8 elements of x * A[r] for ranks r0 .. r0+RB-1,
+// from A's 16-byte chunks av[] of those ranks.
+template <int RANK, int RB>
+__device__ __forceinline__ void lora_accumulate(float (&t)[RANK > 0 ? RANK : 1], uint4 v, const uint4 (&av)[RB], int r0) {
   if constexpr (RANK > 0) {
     float f[8];
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -49,13 +50,12 @@ __device__ __forceinline__ void lora_accumulate(float (&t)[RANK > 0 ? RANK : 1],
       f[2 * j + 1] = bf16_to_f32(w[j] >> 16);
     }
 #pragma unroll
-    for (int r = 0; r < RANK; ++r) {
-      const uint4 av = *reinterpret_cast<const uint4*>(a + r * K + (int64_t)c * 8);
-      const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
+    for (int b = 0; b < RB; ++b) {
+      const uint32_t aw[4] = {av[b].x, av[b].y, av[b].z, av[b].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        t[r] = __builtin_fmaf(f[2 * j], bf16_to_f32(aw[j] & 0xFFFFu), t[r]);
-        t[r] = __builtin_fmaf(f[2 * j + 1], bf16_to_f32(aw[j] >> 16), t[r]);
+        t[r0 + b] = __builtin_fmaf(f[2 * j], bf16_to_f32(aw[j] & 0xFFFFu), t[r0 + b]);
+        t[r0 + b] = __builtin_fmaf(f[2 * j + 1], bf16_to_f32(aw[j] >> 16), t[r0 + b]);
       }
     }
   }
@@ -105,9 +105,32 @@ __device__ __forceinline__ void quant_row(int row, const uint16_t* __restrict__ 
       am = pk_max_u16(am, v[i].y & 0x7FFF7FFFu);
       am = pk_max_u16(am, v[i].z & 0x7FFF7FFFu);
       am = pk_max_u16(am, v[i].w & 0x7FFF7FFFu);
-      lora_accumulate<RANK>(t, v[i], lora_a, K, c);
     } else {
       v[i] = uint4{0, 0, 0, 0};
+    }
+  }
+  if constexpr (RANK > 0) {
+    // A's chunks are loaded 8 ranks at a time, the next batch while this
+    // batch's FMAs run (scheduling barriers keep them apart: left to itself
+    // the compiler keeps only ~5 of them in flight, one L2 round trip per few
+    // ranks). Batches of 16 ranks cost occupancy (2-3 waves per SIMD), which
+    // 2048-row launches need: 28 -> 34 us there.
+    constexpr int RB = RANK > 8 ? 8 : RANK, NB = RANK / RB, G = NC * NB;
+    uint4 ab[2][RB];
+    auto load_a = [&](int g, uint4 (&dst)[RB]) {
+      const int c = min(tid + (g / NB) * THREADS, nchunks - 1), r0 = (g % NB) * RB;
+#pragma unroll
+      for (int b = 0; b < RB; ++b)
+        dst[b] = *reinterpret_cast<const uint4*>(lora_a + (r0 + b) * (int64_t)K + (int64_t)c * 8);
+    };
+    load_a(0, ab[0]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (g + 1 < G) load_a(g + 1, ab[(g + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      const int i = g / NB;
+      if (tid + i * THREADS < nchunks) lora_accumulate<RANK, RB>(t, v[i], ab[g & 1], (g % NB) * RB);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   am = max(am & 0xFFFFu, am >> 16);
