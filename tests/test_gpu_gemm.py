@@ -112,6 +112,25 @@ def test_wide_small_batches_take_64x64_prefill_tiles(N, M):
     check(fp8_matmul(x, wq, sw, bias=bias, lora=lora), x, wq, sw, bias=bias, lora=lora)
 
 
+@pytest.mark.parametrize("M", [17, 48])
+def test_reference_acceptance_inputs_on_64x64_prefill_tiles(weights, M):
+    """The acceptance inputs of inference/cuda_test.py:79-85 (outliers in odd
+    rows, tiny rows) at batch sizes that take the 64x64 prefill tiles on a
+    wide weight; oracle criteria on 4096 sampled output channels, repeat
+    calls bitwise equal."""
+    N, K = 24576, 4096
+    wq, sw = weights(N, K)
+    g = torch.Generator().manual_seed(2000 + M)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    x[1::2, 0] = 1e5
+    x[2::4] *= 2 ** -20
+    x = x.cuda()
+    y = fp8_matmul(x, wq, sw)
+    cols = torch.randperm(N, generator=g)[:4096].sort().values.cuda()
+    check(y[:, cols], x, wq[cols], sw[cols])
+    assert torch.equal(y, fp8_matmul(x, wq, sw)), "second call differs"
+
+
 @pytest.mark.parametrize("N,K", [(256, 4096), (128, 12288), (144, 1024), (144, 2048)])
 @pytest.mark.parametrize("M", [1, 16, 33, 64])
 def test_split_k_decode_path(N, K, M):
