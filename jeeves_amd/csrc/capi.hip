@@ -53,11 +53,16 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K) {
   return JV_OK;
 }
 
-// Bytes of the split-K partials for these sizes (0 when no split).
-int64_t partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
-  if (!jv::decode_kernel_for(M, N, cus)) return 0;
+// Bytes of the decode kernel's split-K partials for these sizes (0 when no
+// split).
+int64_t split_partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
   const int s = jv::decode_plan(M, N, K, cus).splits;
   return s > 1 ? round_up((int64_t)s * M * N * 4, 256) : 0;
+}
+
+// The same for the fp8 GEMM's kernel choice (0 on the prefill kernel).
+int64_t partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
+  return jv::decode_kernel_for(M, N, cus) ? split_partial_bytes(M, N, K, cus) : 0;
 }
 
 // Activation codes for jv_fp8_linear: the packed fragment order whenever the
@@ -217,7 +222,11 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
                   lora_rank, lora_scaling, (uint16_t*)y, ldy, M, N, K, ws, rest, tile_counters, n_counters, s);
 }
 
-int64_t jv_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) { return jv_fp8_gemm_workspace_bytes(M, N, K); }
+int64_t jv_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  const int cus = cu_count_of(-1);
+  if (cus <= 0) return -1;
+  return jv::w8a16_decode_kernel_for(M, N, cus) ? split_partial_bytes(M, N, K, cus) : 0;
+}
 
 int jv_w8a16_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
                     void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
@@ -230,7 +239,7 @@ int jv_w8a16_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, cons
   const int cus = cu_count_of(-1);
   if (cus <= 0) return fail(JV_ERR_HIP, "cannot query the device's compute units");
   hipStream_t s = (hipStream_t)stream;
-  if (M > jv::kDecodeMaxRows)
+  if (!jv::w8a16_decode_kernel_for(M, N, cus))
     return hip_status(jv::w8a16_prefill((const uint16_t*)x, ldx, (const uint8_t*)w, ldw, (int)M, (int)N, (int)K, w_scale,
                                         (const uint16_t*)bias, (uint16_t*)y, ldy, cus, s),
                       "W8A16 prefill GEMM launch");

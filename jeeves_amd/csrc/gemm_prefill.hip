@@ -603,8 +603,10 @@ __global__ __launch_bounds__(512) void gemm_prefill_pp_kernel(const uint8_t* __r
 }
 
 // ---------------------------------------------------------------------------
-// W8A16 parity mode, M > 64: bf16 activations x e4m3 weights (converted to
-// bf16 in registers, exact), v_mfma_f32_32x32x16_bf16, fp32 sums, then
+// W8A16 parity mode, M > 64 or 32-64 tokens on wide weights
+// (w8a16_decode_kernel_for):
+// bf16 activations x e4m3 weights (converted to bf16 in registers, exact),
+// v_mfma_f32_32x32x16_bf16, fp32 sums, then
 // y = bf16(acc * sw[n]) and y = bf16(y + bias[n]) -- the reference's own
 // arithmetic (inference/fp8.py:62-99, :183-184; model/metal_test.py:213).
 // Each 64-deep K stage holds BM token rows of 128 B (bf16) and BN weight rows
@@ -779,6 +781,10 @@ hipError_t w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64
                          const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy, int cu_count,
                          hipStream_t stream) {
   if (K % 64) return hipErrorInvalidValue;
+  // 32-64 tokens over a wide weight (w8a16_decode_kernel_for): 64x64 tiles,
+  // four stages deep (gate+up at 32 tokens 31.3 us; three stages 34.5, six
+  // 34.7: each stage holds only 4 KB of weight).
+  if (M <= kDecodeMaxRows) return launch_w8a16_prefill<64, 64, 2, 2, 4>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 8, stream);
   const int64_t t256 = ((int64_t)(M + 255) / 256) * ((N + 255) / 256);
   if (t256 >= 2 * (int64_t)cu_count)
     return launch_w8a16_prefill<256, 256, 2, 4, 3>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 4, stream);

@@ -24,6 +24,17 @@ inline bool decode_kernel_for(int64_t M, int64_t N, int cu_count) {
   return M <= 16 || 2 * ((N + 63) / 64) < 3 * (int64_t)cu_count;
 }
 
+// The W8A16 prefill tiles stage bf16 token rows, twice the bytes of codes,
+// and win on those wide weights from 32 tokens (gate+up 35.8 vs 60.5 us at
+// 64 tokens, 34.0 vs 43.7 at 48, a tie at 32, 33.6 vs 28.7 at 17; lm_head
+// 285 vs 587 at 64, 256 vs 283 at 32, 250 vs 218 at 17).
+// Where this rule and decode_kernel_for differ the weight has thousands of
+// 16-row tiles, so the decode plan does not split K there: no workspace and
+// no tile counters either way.
+inline bool w8a16_decode_kernel_for(int64_t M, int64_t N, int cu_count) {
+  return M < 32 || decode_kernel_for(M, N, cu_count);
+}
+
 struct DecodePlan {
   int rt;      // 16-row tiles per wave
   int waves;   // waves per workgroup, splitting the workgroup's k range

@@ -18,7 +18,8 @@ import pytest
 import torch
 
 import oracle
-from jeeves_amd.fp8 import FP8Linear, FP8SwiGLU, fp8_matmul_w8a16
+from jeeves_amd import _lib
+from jeeves_amd.fp8 import FP8Linear, FP8SwiGLU, fp8_matmul_w8a16, tile_weight
 from jeeves_amd.fp8_weights import FP8, quantize_rows
 from tests import helpers
 
@@ -111,6 +112,36 @@ def test_w8a16_large_tiles_and_bias(M):
     out = helpers.bits(y[:, sel])
     math = oracle.w8a16_math(helpers.bits(x), helpers.codes_np(wq)[cols], sw.cpu().numpy()[cols])
     assert oracle.bitwise_equal_fraction(out, math) >= MATH_EQUAL_MIN
+
+
+@pytest.mark.parametrize("N", [24576, 24592])
+def test_w8a16_wide_small_batches_take_64x64_prefill_tiles(N):
+    """32-64 tokens over a weight wide enough for 1.5 rounds of 64-channel
+    tiles (the fused gate+up, 24576 channels; 24592 leaves a ragged last
+    tile) run on the 64x64 prefill tiles, 17 tokens on the decode kernel;
+    neither needs a workspace. The exact-rounding acceptance
+    (inference/cuda_test.py:83-90) with outliers and tiny rows, tiled weights
+    equal to row-major ones, the bias bitwise."""
+    K = 4096
+    g = torch.Generator().manual_seed(N)
+    wq, sw = quantize_rows((torch.randn(N, K, generator=g) * (1.0 / K ** 0.5)).cuda())
+    wt = tile_weight(wq)
+    bias = (torch.randn(N, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    cols = columns(N)
+    sel = torch.from_numpy(cols).cuda()
+    for M in (17, 32, 40, 64):
+        assert _lib.lib().jv_w8a16_workspace_bytes(M, N, K) == 0, (N, M)
+        x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+        x[1::2, 0] = 1e5
+        x[2::4] *= 2 ** -20
+        x = x.cuda()
+        y = fp8_matmul_w8a16(x, wq, sw)
+        assert torch.equal(fp8_matmul_w8a16(x, wt, sw, tiled=True), y), (N, M)
+        assert torch.equal(fp8_matmul_w8a16(x, wq, sw, bias=bias), y + bias), (N, M)
+        out = helpers.bits(y[:, sel])
+        exact, _ = f64_parts(x, wq, sw, cols)
+        assert np.isfinite(oracle.bf16_to_f32(out)).all(), (N, M)
+        assert oracle.bitwise_equal_fraction(out, oracle.f64_to_bf16(exact)) >= EXACT_EQUAL_MIN, (N, M)
 
 
 @pytest.mark.parametrize("M", [16, 64, 256])
