@@ -87,6 +87,24 @@ def test_split_for_is_pure_host_logic(product_lib):
     assert L.jv_fp8_counters_needed(16, 4096, 4096, 256) == 0
 
 
+def test_wide_weights_never_split_k(product_lib):
+    """On weights wide enough for 1.5 rounds of 64-channel tiles the FP8 GEMM
+    (from 17 tokens) and the W8A16 GEMM (from 32) leave the decode kernel at
+    different batch sizes; the decode plan never splits K there, so neither
+    choice needs a workspace or tile counters. The split depends on N, K and
+    the CU count only: 16 tokens (always the decode kernel) stand for every
+    batch."""
+    L = product_lib
+    for cus in (32, 80, 104, 256, 304):
+        n_wide = 64 * (-(-3 * cus // 2) - 1) + 1  # smallest N with 2 * ceil(N / 64) >= 3 * cus
+        for N in (n_wide, 24576, 248320):
+            if N < n_wide:
+                continue
+            for K in (128, 4096, 12288, 16384, 65536):
+                assert L.jv_fp8_split_for(16, N, K, cus) == 1, (cus, N, K)
+                assert L.jv_fp8_counters_needed(16, N, K, cus) == 0, (cus, N, K)
+
+
 def test_packed_layout_sizes_are_host_logic(product_lib):
     L = product_lib
     assert L.jv_fp8_packed_codes_bytes(16, 4096) == 16 * 4096
