@@ -93,14 +93,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
 
   // One burst of up to UNROLL k steps: all its loads are issued, then the
   // MFMAs consume them. A full burst is straight-line code, so each step's
-  // MFMAs wait only for that step's data; a short last burst guards each step.
+  // MFMAs wait only for that step's data; the steps after the last full burst run one per call.
   auto burst = [&](int s, auto full) {
     constexpr bool FULL = decltype(full)::value;
     i32x4 wa[UNROLL][RT][2];
     i32x4 xa[UNROLL][MT][2];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      if (!FULL && s + u >= s_end) break;
+      if (!FULL && u >= 1) break;
       const int64_t off = (int64_t)(s + u) * 128;
       const int64_t woff = PACKW ? (int64_t)(s + u) * 2048 : off;
 #pragma unroll
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
     if constexpr (FULL) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      if (!FULL && s + u >= s_end) break;
+      if (!FULL && u >= 1) break;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const i32x8 b = cat8(xa[u][mt][0], xa[u][mt][1]);
@@ -129,7 +129,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   };
   int s = s_begin;
   for (; s + UNROLL <= s_end; s += UNROLL) burst(s, std::true_type{});
-  if (s < s_end) burst(s, std::false_type{});
+  // The remaining steps one at a time: a guarded burst of two or more steps
+  // gave wrong sums on gfx950 (k ranges whose length leaves 2-3 steps after
+  // the full bursts, e.g. K = 6656 over 8 waves), one-step bursts are exact.
+  for (; s < s_end; ++s) burst(s, std::false_type{});
 
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)

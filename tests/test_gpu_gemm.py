@@ -170,6 +170,21 @@ def test_decode_short_k(N, K, M):
     check(fp8_matmul_quantized(xq, sx, wq, sw), x, wq, sw)
 
 
+@pytest.mark.parametrize("M,N,K", [(7, 16, 6656), (7, 4096, 6656), (16, 96, 6656), (7, 16, 4224), (7, 16, 4608),
+                                   (7, 4096, 6528), (7, 4096, 5632), (7, 4096, 3968), (7, 4096, 1152), (33, 4096, 6656)])
+def test_decode_k_ranges_with_short_tails(M, N, K):
+    """k ranges whose length leaves 1-3 steps after the full bursts of a wave
+    (K = 6656 over 8 waves: 6 or 7 steps, bursts of 4), with and without
+    split-K: the tail steps once gave wrong sums (a seeded shape sweep found
+    M=7, N=16, K=6656), both decode entry points."""
+    x = synthetic.activations_heavy_tail(M, K, 95 + M)
+    wq, sw = quantize_rows(synthetic.weight(N, K, 96).cuda())
+    x = x.cuda()
+    check(fp8_matmul(x, wq, sw), x, wq, sw)
+    xq, sx = quantize_rows(x)
+    check(fp8_matmul_quantized(xq, sx, wq, sw), x, wq, sw)
+
+
 @pytest.mark.parametrize("name", list(synthetic.SHAPES))
 @pytest.mark.parametrize("M", [512, 2048])
 def test_prefill_workload_shapes(name, M):
