@@ -1,11 +1,16 @@
 // The fused output epilogue shared by the decode and prefill GEMMs:
 //
-//   y[m,n] = bf16( (acc * sx[m]) * sw[n] + bias[n] + lora_scale * sum_r t[m,r] * B[n,r] )
+//   v[m,n]   = (acc * sx[m]) * sw[n] + lora_scale * sum_r t[m,r] * B[n,r]
+//   y[m,n]   = bf16(v)                          without a bias
+//   y[m,n]   = bf16(bf16(v) + bias[n])          with a bias
 //
-// acc * sx * sw is the scale epilogue of _fp8_matmul (inference/fp8.py:83,87);
-// the bias is FP8Linear.forward's (inference/fp8.py:183-184); the LoRA term is
-// LoRALinear.forward's (model/lora.py:122-133) with t = x A^T computed by the
-// quantizer. The sum is rounded to bf16 once.
+// acc * sx * sw is the scale epilogue of _fp8_matmul (inference/fp8.py:83,87),
+// rounded to bf16 as fp8_matmul returns it; the bias is then added to that bf16
+// output in bf16, as FP8Linear.forward does (inference/fp8.py:183-184), so a
+// biased call is bitwise the unbiased call plus the bias. The LoRA term is
+// LoRALinear.forward's (model/lora.py:122-133) with t = x A^T from the
+// quantizer in fp32, folded into the same rounding as the GEMM (the reference
+// merges LoRA before FP8 export, so it never runs one on an FP8 base).
 #pragma once
 
 #include "fp8_common.h"
@@ -23,12 +28,16 @@ struct Epilogue {
   int64_t ldy;
 };
 
-// biasn: the bias of channel n, already loaded (used only when ep.bias is set).
+// The value the caller rounds to bf16 once more: v itself, or bf16(v) + bias.
+// biasn: the bias of the channel, already loaded (used only when ep.bias is set).
+__device__ __forceinline__ float with_bias(const Epilogue& ep, float v, float biasn) {
+  return ep.bias ? bf16_to_f32(f32_to_bf16(v)) + biasn : v;
+}
+
 template <int RANK>
 __device__ __forceinline__ float epilogue_value(const Epilogue& ep, float acc, int m, int n, float sxm, float swn,
                                                 float biasn) {
   float v = (acc * sxm) * swn;
-  if (ep.bias) v += biasn;
   if constexpr (RANK > 0) {
     const float* t = ep.lora_t + (int64_t)m * RANK;
     const uint16_t* b = ep.lora_b + (int64_t)n * RANK;
@@ -37,12 +46,7 @@ __device__ __forceinline__ float epilogue_value(const Epilogue& ep, float acc, i
     for (int r = 0; r < RANK; ++r) l = __builtin_fmaf(t[r], bf16_to_f32(b[r]), l);
     v += l * ep.lora_scale;
   }
-  return v;
+  return with_bias(ep, v, biasn);
 }
 
-// Same with the bias read here.
-template <int RANK>
-__device__ __forceinline__ float epilogue_value(const Epilogue& ep, float acc, int m, int n, float sxm, float swn) {
-  return epilogue_value<RANK>(ep, acc, m, n, sxm, swn, ep.bias ? bf16_to_f32(ep.bias[n]) : 0.0f);
-}
 }  // namespace jv

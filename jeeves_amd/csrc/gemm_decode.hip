@@ -39,7 +39,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   __shared__ f32x4 red[WAVES][RT * MT][64];
   __shared__ int is_last;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Wave-uniform in a scalar register, so the k range [s_begin, s_end) and the
+  // tail guards below are scalar branches. Computed in a vector register the
+  // guards become EXEC-masked regions, and gfx950 writes an MFMA's result
+  // even with EXEC = 0: a guarded-off tail step's MFMA then adds whatever its
+  // unloaded operand registers hold (address bits, found with the assembly
+  // scan in the kernel-resource tests).
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int group = blockIdx.x;
   const int split = blockIdx.y;
   const int n0 = group * 16 * RT;
@@ -93,14 +99,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
 
   // One burst of up to UNROLL k steps: all its loads are issued, then the
   // MFMAs consume them. A full burst is straight-line code, so each step's
-  // MFMAs wait only for that step's data; the steps after the last full burst run one per call.
+  // MFMAs wait only for that step's data; the last, partial burst guards each
+  // step with a scalar branch (s and s_end are wave-uniform).
   auto burst = [&](int s, auto full) {
     constexpr bool FULL = decltype(full)::value;
     i32x4 wa[UNROLL][RT][2];
     i32x4 xa[UNROLL][MT][2];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      if (!FULL && u >= 1) break;
+      if (!FULL && s + u >= s_end) break;
       const int64_t off = (int64_t)(s + u) * 128;
       const int64_t woff = PACKW ? (int64_t)(s + u) * 2048 : off;
 #pragma unroll
@@ -118,7 +125,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
     if constexpr (FULL) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      if (!FULL && u >= 1) break;
+      if (!FULL && s + u >= s_end) break;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const i32x8 b = cat8(xa[u][mt][0], xa[u][mt][1]);
@@ -129,10 +136,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   };
   int s = s_begin;
   for (; s + UNROLL <= s_end; s += UNROLL) burst(s, std::true_type{});
-  // The remaining steps one at a time: a guarded burst of two or more steps
-  // gave wrong sums on gfx950 (k ranges whose length leaves 2-3 steps after
-  // the full bursts, e.g. K = 6656 over 8 waves), one-step bursts are exact.
-  for (; s < s_end; ++s) burst(s, std::false_type{});
+  if (s < s_end) burst(s, std::false_type{});
 
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
@@ -165,15 +169,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   }
   if (splits == 1) return;
 
-  // Every partial store of this workgroup has completed (s_waitcnt) before
-  // its count is added; the workgroup that sees count splits-1 reads all
-  // partials with device-coherent loads.
-  __builtin_amdgcn_s_waitcnt(0);
+  // The workgroup that sees count splits-1 sums every split's partials in
+  // split order and resets the counter.
+  // Release: each thread's partial stores are ordered at device scope before
+  // the barrier, and thread 0's acq_rel count after it (the barrier carries
+  // the workgroup's stores to thread 0); the reducing workgroup acquires at
+  // device scope before it reads (inference/fp8.py:94 counts with acq_rel).
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
   if (threadIdx.x == 0)
-    is_last = __hip_atomic_fetch_add(counters + group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+    is_last = __hip_atomic_fetch_add(counters + group, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
   __syncthreads();
   if (!is_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int idx = (int)threadIdx.x + j * kThreads;

@@ -141,7 +141,7 @@ __device__ __forceinline__ f32x16 lora_block(i32x4 b, const float4 (&t)[2]) {
 // Epilogue of both FP8 prefill kernels. 32x32 MFMA output layout: lane l
 // holds column l % 32 (a token) and, in register r, row 8*(r/4) + 4*(l/32) +
 // r%4 (a channel): each register quad is 4 consecutive channels of one token.
-// y = bf16((acc * sx[m]) * sw[n] (+ bias[n]) (+ lora_scale * l[n, m])). The
+// y = bf16((acc * sx[m]) * sw[n] (+ lora_scale * l[n, m])), then + bias[n] in bf16. The
 // finished bf16 tile goes through LDS ([BM tokens][BN channels], 16-byte
 // chunk c of row r stored at chunk c ^ (r % OUT_CH)) so that global stores are
 // 16 bytes per lane over whole row segments. The caller's operand reads and
@@ -180,8 +180,9 @@ __device__ __forceinline__ void store_tile(uint8_t* lds, const float* scale_lds,
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[e] = epilogue_value<0>(ep, acc[j][i][4 * q + e], m, min(n + e, N - 1), sxm[i], sw4[e]);
+          v[e] = (acc[j][i][4 * q + e] * sxm[i]) * sw4[e];
           if constexpr (RANK > 0) v[e] += lora[4 * q + e] * ep.lora_scale;
+          if (ep.bias) v[e] = with_bias(ep, v[e], bf16_to_f32(ep.bias[min(n + e, N - 1)]));
         }
         const int chunk = (nl >> 3) ^ (ml % OUT_CH);
         *reinterpret_cast<uint2*>(lds + ml * (BN * 2) + chunk * 16 + (nl & 4) * 2) =

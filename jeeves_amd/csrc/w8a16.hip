@@ -38,7 +38,10 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
   __shared__ f32x4 red[W][RT * MT][64];
   __shared__ int is_last;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Wave-uniform (scalar register): the burst guards below are scalar
+  // branches, never EXEC-masked regions, whose MFMAs gfx950 would still
+  // execute with EXEC = 0 (see gemm_decode_kernel).
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int group = blockIdx.x, split = blockIdx.y;
   const int n0 = group * 16 * RT;
 
@@ -147,15 +150,19 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
   }
   if (splits == 1) return;
 
-  // Every partial store of this workgroup has completed before its count is
-  // added; the workgroup that sees count splits-1 sums all partials in split
-  // order with device-coherent loads and resets the counter.
-  __builtin_amdgcn_s_waitcnt(0);
+  // The workgroup that sees count splits-1 sums every split's partials in
+  // split order and resets the counter.
+  // Release: each thread's partial stores are ordered at device scope before
+  // the barrier, and thread 0's acq_rel count after it (the barrier carries
+  // the workgroup's stores to thread 0); the reducing workgroup acquires at
+  // device scope before it reads (inference/fp8.py:94 counts with acq_rel).
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
   if (threadIdx.x == 0)
-    is_last = __hip_atomic_fetch_add(counters + group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+    is_last = __hip_atomic_fetch_add(counters + group, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
   __syncthreads();
   if (!is_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int idx = (int)threadIdx.x + j * kThreads;

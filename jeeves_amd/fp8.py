@@ -160,6 +160,19 @@ def untile_weight(tiled: torch.Tensor) -> torch.Tensor:
     return out.view(tiled.dtype)
 
 
+def _tile_into(codes: torch.Tensor, out: torch.Tensor) -> None:
+    """``tile_weight`` written into an existing buffer (same device and size)."""
+    N, K = codes.shape
+    src = codes.view(torch.uint8)
+    if codes.device.type != "cuda":
+        out.copy_(tile_weight(codes).view(torch.uint8))
+        return
+    if not _rows_aligned(src, 1):
+        src = src.contiguous()
+    with torch.cuda.device(codes.device):
+        _lib.check(_lib.lib().jv_fp8_tile_weight(src.data_ptr(), src.stride(0), N, K, out.data_ptr(), _stream(codes.device)))
+
+
 def _check_lora(lora, K: int, N: int):
     if lora is None:
         return None, None, 0, 0.0
@@ -362,16 +375,21 @@ def swiglu_quantize(gate: torch.Tensor, up: torch.Tensor, *, lora_a: torch.Tenso
 
 
 class FP8Linear(nn.Module):
-    """``inference/fp8.py:151-185``: buffers ``weight`` (float8_e4m3fn [N,K])
-    and ``scale`` (float32 [N]), optional bf16 ``bias``. ``set_lora`` attaches
-    a LoRA adapter (``model/lora.py:122-133``) that the GEMM epilogue adds.
+    """``inference/fp8.py:151-185``: buffers ``weight`` (float8_e4m3fn [N,K],
+    row-major, as the reference keeps it) and ``scale`` (float32 [N]),
+    optional bf16 ``bias``. ``set_lora`` attaches a LoRA adapter
+    (``model/lora.py:122-133``) that the GEMM epilogue adds.
 
-    When the shape allows (``tileable``: N % 16 == 0, K % 128 == 0) the
-    ``weight`` buffer holds the codes in the ``tile_weight`` layout the decode
-    kernels read fastest (``tiled`` is True). The state dict still carries
-    row-major codes under ``weight`` (converted on save and on load), and
-    ``load_codes``/``load_weight`` take row-major codes, so checkpoints and
-    callers see the reference's format; ``codes()`` returns them row-major.
+    When the shape allows (``tileable``: N % 16 == 0, K % 128 == 0) and
+    ``TILED_COPY`` is set, the kernels read a second copy of the codes,
+    ``tiled_codes`` (uint8 [N,K] in the ``tile_weight`` layout), the way the
+    reference's Metal module keeps ``tiled_codes`` for its kernel
+    (``inference/fp8_metal.py:17``): a decode wave then loads one contiguous
+    1 KB per instruction. The copy is not part of the state dict; it is
+    rebuilt from ``weight`` whenever ``weight`` changed (an in-place write, a
+    new tensor, ``load_state_dict``), so ``weight`` stays the one source of
+    truth. It doubles the codes' HBM footprint; with ``TILED_COPY = False``
+    the kernels read ``weight`` itself (``tiled`` is then False).
 
     ``activations`` picks the arithmetic: ``"fp8"`` (default) quantizes the
     activations per token and runs the FP8 x FP8 GEMM; ``"bf16"`` is the
@@ -380,6 +398,7 @@ class FP8Linear(nn.Module):
     """
 
     ACTIVATIONS = ("fp8", "bf16")
+    TILED_COPY = True
 
     def __init__(self, in_features: int, out_features: int, bias: bool = False, device: torch.device | str | None = None):
         super().__init__()
@@ -387,28 +406,38 @@ class FP8Linear(nn.Module):
         self.register_buffer("scale", torch.empty(out_features, dtype=torch.float32, device=device))
         self.bias = nn.Parameter(torch.empty(out_features, dtype=torch.bfloat16, device=device), requires_grad=False) if bias else None
         self.in_features, self.out_features = in_features, out_features
-        self.tiled = tileable(out_features, in_features)
+        self.tiled = self.TILED_COPY and tileable(out_features, in_features)
+        self.register_buffer("tiled_codes", torch.empty(out_features, in_features, dtype=torch.uint8, device=device)
+                             if self.tiled else None, persistent=False)
+        # (address, version) of the weight the tiled copy was made from
+        self._tiled_from: tuple[int, int] | None = None
         self.lora: tuple[torch.Tensor, torch.Tensor, float] | None = None
         self.activations = "fp8"
-        self._register_state_dict_hook(FP8Linear._rowmajor_state)
-        self._register_load_state_dict_pre_hook(FP8Linear._tile_loaded_state, with_module=True)
+        self.register_load_state_dict_post_hook(FP8Linear._retile_loaded)
 
     @staticmethod
-    def _rowmajor_state(module: "FP8Linear", state: dict, prefix: str, local_metadata) -> None:
-        key = prefix + "weight"
-        if module.tiled and key in state and state[key].device.type != "meta":
-            state[key] = untile_weight(state[key])
+    def _retile_loaded(module: "FP8Linear", incompatible_keys) -> None:
+        if module.weight.device.type == "cuda":
+            module.kernel_weight()
 
-    @staticmethod
-    def _tile_loaded_state(module: "FP8Linear", state: dict, prefix: str, local_metadata, strict, missing_keys,
-                           unexpected_keys, error_msgs) -> None:
-        key = prefix + "weight"
-        if module.tiled and key in state and tuple(state[key].shape) == (module.out_features, module.in_features):
-            state[key] = tile_weight(state[key].to(module.weight.device))
+    def _weight_key(self) -> tuple[int, int]:
+        return self.weight.data_ptr(), self.weight._version
+
+    def kernel_weight(self) -> tuple[torch.Tensor, bool]:
+        """The codes the kernels read and whether they are tiled: the tiled
+        copy, rebuilt first if ``weight`` changed since it was made, or
+        ``weight`` itself."""
+        if not self.tiled:
+            return self.weight, False
+        key = self._weight_key()
+        if self._tiled_from != key:
+            _tile_into(self.weight, self.tiled_codes)
+            self._tiled_from = key
+        return self.tiled_codes, True
 
     def codes(self) -> torch.Tensor:
-        """The e4m3 codes, row-major [N, K] (a converted copy when tiled)."""
-        return untile_weight(self.weight) if self.tiled else self.weight
+        """The e4m3 codes, row-major [N, K] (``weight``)."""
+        return self.weight
 
     def set_activations(self, mode: str) -> None:
         """``"fp8"`` (per-token e4m3 activations) or ``"bf16"`` (W8A16 parity mode)."""
@@ -420,11 +449,10 @@ class FP8Linear(nn.Module):
 
     @torch.no_grad()
     def load_codes(self, codes: torch.Tensor, scale: torch.Tensor) -> None:
-        """Row-major codes [N, K] and their scales (stored tiled when ``tiled``)."""
-        if self.tiled:
-            codes = tile_weight(codes.to(self.weight.device))
         self.weight.copy_(codes)
         self.scale.copy_(scale)
+        if self.weight.device.type == "cuda":
+            self.kernel_weight()
 
     @torch.no_grad()
     def load_weight(self, weight: torch.Tensor) -> None:
@@ -440,16 +468,22 @@ class FP8Linear(nn.Module):
     @classmethod
     def concatenated(cls, parts: list["FP8Linear"]) -> "FP8Linear":
         """One linear over the parts' output rows (``inference/fp8.py:168-175``);
-        the parts become views of its buffers. Tiles are whole 16-row groups,
-        so tiled parts concatenate as they are; if any part is row-major the
-        merged buffer is row-major and every part converts to it."""
+        the parts' ``weight`` and ``scale`` become views of the merged buffers.
+        Tiles are whole 16-row groups, so the parts' tiled copies concatenate
+        as they are and become views of the merged copy too; if any part
+        cannot tile, the merged module and every part read row-major codes."""
         sizes = [p.out_features for p in parts]
         merged = cls(parts[0].in_features, sum(sizes), device="meta")
-        merged.tiled = merged.tiled and all(p.tiled for p in parts)
-        weights = [p.weight if merged.tiled else p.codes() for p in parts]
-        merged.weight, merged.scale = torch.cat(weights), torch.cat([p.scale for p in parts])
-        for p, weight, scale in zip(parts, merged.weight.split(sizes), merged.scale.split(sizes)):
-            p.weight, p.scale, p.tiled = weight, scale, merged.tiled
+        tiled = merged.tiled and all(p.tiled for p in parts)
+        copies = [p.kernel_weight()[0] for p in parts] if tiled else None
+        merged.weight, merged.scale = torch.cat([p.weight for p in parts]), torch.cat([p.scale for p in parts])
+        merged.tiled = tiled
+        merged.tiled_codes = torch.cat(copies) if tiled else None
+        merged._tiled_from = merged._weight_key() if tiled else None
+        tiles = merged.tiled_codes.split(sizes) if tiled else [None] * len(parts)
+        for p, weight, scale, t in zip(parts, merged.weight.split(sizes), merged.scale.split(sizes), tiles):
+            p.weight, p.scale, p.tiled, p.tiled_codes = weight, scale, tiled, t
+            p._tiled_from = p._weight_key() if tiled else None
         return merged
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -457,10 +491,11 @@ class FP8Linear(nn.Module):
         x2 = x.reshape(-1, shape[-1]).to(torch.bfloat16)
         if x2.stride(-1) != 1:
             x2 = x2.contiguous()
+        w, tiled = self.kernel_weight()
         if self.activations == "bf16":
-            y = fp8_matmul_w8a16(x2, self.weight, self.scale, bias=self.bias, tiled=self.tiled)
+            y = fp8_matmul_w8a16(x2, w, self.scale, bias=self.bias, tiled=tiled)
         else:
-            y = fp8_matmul(x2, self.weight, self.scale, bias=self.bias, lora=self.lora, tiled=self.tiled)
+            y = fp8_matmul(x2, w, self.scale, bias=self.bias, lora=self.lora, tiled=tiled)
         return y.view(*shape[:-1], self.out_features)
 
 
@@ -483,7 +518,8 @@ class FP8SwiGLU(nn.Module):
         if self.down.activations == "bf16":
             # W8A16 parity mode: h = silu(gate) * up in bf16 feeds the down GEMM as is.
             h = swiglu_quantize(gu[:, :inter], gu[:, inter:], return_h=True)[-1]
-            y = fp8_matmul_w8a16(h, self.down.weight, self.down.scale, bias=self.down.bias, tiled=self.down.tiled)
+            w, tiled = self.down.kernel_weight()
+            y = fp8_matmul_w8a16(h, w, self.down.scale, bias=self.down.bias, tiled=tiled)
             return y.view(*shape[:-1], self.down.out_features)
         lora_a = self.down.lora[0] if self.down.lora is not None else None
         # The down GEMM reads its codes fastest in fragment order (both the
@@ -492,10 +528,11 @@ class FP8SwiGLU(nn.Module):
         packed = M > 0 and inter % BLOCK_K == 0 and inter <= QUANT_MAX_PACKED_COLS
         out = swiglu_quantize(gu[:, :inter], gu[:, inter:], lora_a=lora_a, packed=packed)
         lora_t = out[2] if lora_a is not None else None
-        y = fp8_matmul_quantized(out[0], out[1], self.down.weight, self.down.scale, bias=self.down.bias, lora_t=lora_t,
+        w, tiled = self.down.kernel_weight()
+        y = fp8_matmul_quantized(out[0], out[1], w, self.down.scale, bias=self.down.bias, lora_t=lora_t,
                                  lora_b=self.down.lora[1] if lora_a is not None else None,
                                  lora_scaling=self.down.lora[2] if lora_a is not None else 0.0,
-                                 packed_rows=M if packed else None, tiled=self.down.tiled)
+                                 packed_rows=M if packed else None, tiled=tiled)
         return y.view(*shape[:-1], self.down.out_features)
 
 

@@ -31,7 +31,10 @@ function                    pinned by
                             argument (below)
 ``dequant_matmul_f64``      linearity and brute force on tiny shapes
 ``w8a16_math``              brute force on tiny shapes (float32 sums)
-``lora_f64``/``swiglu_f64`` closed forms evaluated on tiny shapes by loops
+``add_bias_bf16``           torch's bf16 add on dense random and edge pairs
+``lora_f64``                closed form evaluated on tiny shapes by loops
+``swiglu_bf16``             torch's ``F.silu(gate) * up`` on every bf16 gate
+                            value (65536) times random bf16 ups
 ==========================  ===================================================
 """
 
@@ -45,7 +48,7 @@ __all__ = [
     "bf16_to_f32", "f32_to_bf16", "f64_to_bf16",
     "quantize_rows", "quantize_row_blocks_on_cpu", "quantizable",
     "gemm_exact_f64", "gemm_exact_bf16", "dequant_matmul_f64", "dequant_matmul_f32", "w8a16_math",
-    "lora_f64", "silu_f64", "swiglu_bf16",
+    "add_bias_bf16", "lora_f64", "silu_f32", "swiglu_bf16",
     "rel_l2", "bitwise_equal_fraction", "within_metal_bound",
 ]
 
@@ -204,11 +207,17 @@ def gemm_exact_f64(xq: np.ndarray, sx: np.ndarray, wq: np.ndarray, sw: np.ndarra
 
 
 def gemm_exact_bf16(xq, sx, wq, sw, bias_bits=None) -> np.ndarray:
-    """Exact result rounded once to bf16 (via float, as torch rounds double)."""
-    y = gemm_exact_f64(xq, sx, wq, sw)
-    if bias_bits is not None:
-        y = y + bf16_to_f32(bias_bits).astype(np.float64)[None, :]
-    return f64_to_bf16(y)
+    """Exact result rounded once to bf16 (via float, as torch rounds double);
+    with a bias, that bf16 output plus the bias as ``FP8Linear.forward`` adds
+    it (``add_bias_bf16``)."""
+    y = f64_to_bf16(gemm_exact_f64(xq, sx, wq, sw))
+    return y if bias_bits is None else add_bias_bf16(y, bias_bits)
+
+
+def add_bias_bf16(y_bits: np.ndarray, bias_bits: np.ndarray) -> np.ndarray:
+    """``y + bias`` on bf16 tensors (``inference/fp8.py:183-184``): the sum of
+    the two bf16 values in float32, rounded to bf16 (torch's bf16 add)."""
+    return f32_to_bf16(bf16_to_f32(y_bits) + bf16_to_f32(bias_bits)[None, :])
 
 
 def dequant_matmul_f64(xq, sx, wq, sw) -> np.ndarray:
@@ -238,17 +247,20 @@ def lora_f64(x: np.ndarray, a: np.ndarray, b: np.ndarray, scaling: float) -> np.
     return (x @ np.asarray(a, np.float64).T) @ (np.asarray(b, np.float64) * scaling).T
 
 
-def silu_f64(g: np.ndarray) -> np.ndarray:
-    g = np.asarray(g, np.float64)
-    return g / (1.0 + np.exp(-g))
+def silu_f32(g: np.ndarray) -> np.ndarray:
+    """``g / (1 + exp(-g))`` in float32, as torch evaluates ``F.silu`` on bf16
+    (float32 arithmetic; exp(-g) overflows to inf for g < -88.7, giving -0)."""
+    g = np.asarray(g, np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        return (g / (np.float32(1.0) + np.exp(-g))).astype(np.float32)
 
 
 def swiglu_bf16(gate_bits: np.ndarray, up_bits: np.ndarray) -> np.ndarray:
-    """``F.silu(gate) * up`` on bf16 tensors (``model/model.py:583``): silu is
-    computed in float and rounded to bf16, then the bf16 product is rounded."""
-    g = bf16_to_f32(gate_bits).astype(np.float64)
-    s = f64_to_bf16(silu_f64(g))
-    return f64_to_bf16(bf16_to_f32(s).astype(np.float64) * bf16_to_f32(up_bits).astype(np.float64))
+    """``F.silu(gate) * up`` on bf16 tensors (``model/model.py:583``): silu in
+    float32 rounded to bf16, then the product of the two bf16 values (exact in
+    float32) rounded to bf16."""
+    s = f32_to_bf16(silu_f32(bf16_to_f32(gate_bits)))
+    return f32_to_bf16(bf16_to_f32(s) * bf16_to_f32(up_bits))
 
 
 # ---------------------------------------------------------------------------

@@ -91,32 +91,39 @@ BOUND_MAGNITUDE = 2.0 ** -11  # |out-exact| <= |exact| 2^-8 + magnitude * this
 def gemm_criteria(out_bits: np.ndarray, xq, sx, wq, sw, bias_bits=None, lora_term=None) -> dict:
     """The acceptance numbers for one GEMM output:
     * equal: share bitwise equal to the exact result rounded once to bf16
-      (inference/cuda_test.py:87-91);
+      (inference/cuda_test.py:87-91); with a bias, that bf16 result plus the
+      bias in bf16, as FP8Linear.forward adds it (inference/fp8.py:183-184);
     * rel_l2: vs the dequantize-then-matmul output, which like every output
       of the path is bf16 (rounding alone puts a bf16 result ~1.5e-3 away
       from its unrounded value, so the comparison is bf16 to bf16);
     * bound: |out - exact| <= |exact| 2^-8 + magnitude * BOUND_MAGNITUDE, the
       form of model/metal_test.py:219-221 with the magnitude term sized for the
-      FP8 MFMA's in-instruction alignment instead of fp32 summation (2^-20)."""
+      FP8 MFMA's in-instruction alignment instead of fp32 summation (2^-20),
+      plus, with a bias, the bf16 rounding of the GEMM output before the bias
+      is added (2^-8 of its magnitude)."""
     exact = oracle.gemm_exact_f64(xq, sx, wq, sw)
-    if bias_bits is not None:
-        exact = exact + oracle.bf16_to_f32(bias_bits).astype(np.float64)[None, :]
     if lora_term is not None:
         exact = exact + lora_term
     exact_bits = oracle.f64_to_bf16(exact)
-    out = oracle.bf16_to_f32(out_bits).astype(np.float64)
     xd = np.abs(oracle.e4m3_decode(xq).astype(np.float64) * np.asarray(sx, np.float64)[:, None])
     wd = np.abs(oracle.e4m3_decode(wq).astype(np.float64) * np.asarray(sw, np.float64)[:, None])
     magnitude = xd @ wd.T
-    if bias_bits is not None:
-        magnitude = magnitude + np.abs(oracle.bf16_to_f32(bias_bits).astype(np.float64))[None, :]
     if lora_term is not None:
         magnitude = magnitude + np.abs(lora_term)
+    slack = 0.0
+    if bias_bits is not None:
+        slack = np.abs(exact) * 2.0 ** -8
+        exact_bits = oracle.add_bias_bf16(exact_bits, bias_bits)
+        bias = oracle.bf16_to_f32(bias_bits).astype(np.float64)[None, :]
+        exact = exact + bias
+        magnitude = magnitude + np.abs(bias)
+    out = oracle.bf16_to_f32(out_bits).astype(np.float64)
     finite = np.isfinite(exact)
     exact_rounded = oracle.bf16_to_f32(exact_bits).astype(np.float64)
+    bound_mag = magnitude * (BOUND_MAGNITUDE / 2.0 ** -20) + slack * 2.0 ** 20
     return {
         "equal": oracle.bitwise_equal_fraction(out_bits, exact_bits),
         "rel_l2": oracle.rel_l2(out[finite], exact_rounded[finite]) if finite.any() else 0.0,
-        "bound": oracle.within_metal_bound(out[finite], exact[finite], magnitude[finite] * (BOUND_MAGNITUDE / 2.0 ** -20)) if finite.any() else True,
+        "bound": oracle.within_metal_bound(out[finite], exact[finite], bound_mag[finite]) if finite.any() else True,
         "finite_match": bool((np.isfinite(out) == finite).all()),
     }

@@ -86,7 +86,10 @@ def test_load_tensors_round_trip(tmp_path):
     assert isinstance(m.q, FP8Linear) and isinstance(m.o, FP8Linear) and isinstance(m.head, nn.Linear)
     loaded, unexpected = fp8_checkpoint.load_tensors(m, [dst], FP8Linear)
     assert unexpected == []
-    assert loaded == {"q.weight", "q.scale", "o.weight", "o.scale", "o.bias", "head.weight", "norm.weight", "norm.bias"}
+    # every buffer of a loaded FP8 linear counts as loaded, the kernels' tiled
+    # copy included (inference/fp8_checkpoint.py:78 adds named_buffers())
+    assert loaded == {"q.weight", "q.scale", "q.tiled_codes", "o.weight", "o.scale", "o.tiled_codes", "o.bias",
+                      "head.weight", "norm.weight", "norm.bias"}
     want_codes, want_scale = oracle.quantize_rows(tensors["q.weight"].float().numpy())
     assert np.array_equal(m.q.codes().view(torch.uint8).numpy(), want_codes)
     assert np.array_equal(m.q.scale.numpy(), want_scale)

@@ -171,12 +171,16 @@ def test_decode_short_k(N, K, M):
 
 
 @pytest.mark.parametrize("M,N,K", [(7, 16, 6656), (7, 4096, 6656), (16, 96, 6656), (7, 16, 4224), (7, 16, 4608),
-                                   (7, 4096, 6528), (7, 4096, 5632), (7, 4096, 3968), (7, 4096, 1152), (33, 4096, 6656)])
+                                   (7, 4096, 6528), (7, 4096, 5632), (7, 4096, 3968), (7, 4096, 1152), (33, 4096, 6656),
+                                   (31, 16, 2688), (3, 1040, 2432)])
 def test_decode_k_ranges_with_short_tails(M, N, K):
     """k ranges whose length leaves 1-3 steps after the full bursts of a wave
     (K = 6656 over 8 waves: 6 or 7 steps, bursts of 4), with and without
-    split-K: the tail steps once gave wrong sums (a seeded shape sweep found
-    M=7, N=16, K=6656), both decode entry points."""
+    split-K, both decode entry points. The last, partial burst guards its
+    steps with scalar branches; when the k bounds sat in vector registers the
+    guards were EXEC-masked and a guarded-off step's MFMA still added its
+    unloaded operand registers (a seeded shape sweep found M=7, N=16,
+    K=6656)."""
     x = synthetic.activations_heavy_tail(M, K, 95 + M)
     wq, sw = quantize_rows(synthetic.weight(N, K, 96).cuda())
     x = x.cuda()
@@ -194,7 +198,7 @@ def test_prefill_workload_shapes(name, M):
     check(fp8_matmul(x, wq, sw), x, wq, sw)
 
 
-@pytest.mark.parametrize("name", ["k", "gate_up", "down"])
+@pytest.mark.parametrize("name", ["q", "k", "gate_up", "down"])
 def test_prefill_8192_rows_by_sampled_rows_and_slices(name):
     """M = 8192 is too large for a float64 oracle of every row: check 96
     sampled rows against the oracle, and that row slices computed alone are

@@ -2,7 +2,7 @@
 weights: every kernel reads the same codes from it, so outputs are bitwise
 identical on every regime -- decode (1-4 token tiles, 4 and 8 waves, split K),
 prefill (each tile shape the dispatcher picks), the W8A16 parity mode, packed
-activation codes, bias and LoRA -- and FP8Linear, which stores its weights
+activation codes, bias and LoRA -- and FP8Linear, which keeps a tiled copy of its weights
 tiled, keeps the reference's row-major state dict and concatenation."""
 
 from __future__ import annotations
@@ -85,11 +85,13 @@ def test_bias_lora_packed_and_w8a16_tiled(weights, M):
                            fp8_matmul_quantized(codes, scales, wq2, sw2, packed_rows=M))
 
 
-def test_module_keeps_row_major_state_and_merges():
-    """FP8Linear stores tiled codes but its state dict, load_state_dict,
-    load_codes and codes() speak row-major (the reference's format); tiled
-    parts concatenate as they are, a part that cannot tile makes the merge
-    row-major, and every part's output is unchanged by the merge."""
+def test_module_keeps_row_major_weight_and_merges():
+    """FP8Linear.weight, its state dict, load_state_dict, load_codes and
+    codes() all hold the reference's row-major codes; the kernels read the
+    tiled copy. Tiled parts concatenate as they are (the parts' copies become
+    views of the merged copy), a part that cannot tile makes the merge
+    row-major, every part's output is unchanged by the merge, and an in-place
+    write to a part's weight reaches the merged module's kernels too."""
     K = 4096
     parts = [FP8Linear(K, n, device="cuda") for n in (2048, 1024, 1024)]
     for i, p in enumerate(parts):
@@ -97,8 +99,9 @@ def test_module_keeps_row_major_state_and_merges():
         assert p.tiled
     codes = [quantize_rows(synthetic.weight(p.out_features, K, 5400 + i).cuda())[0] for i, p in enumerate(parts)]
     for p, c in zip(parts, codes):
-        assert torch.equal(p.codes().view(torch.uint8), c.view(torch.uint8))
+        assert torch.equal(p.weight.view(torch.uint8), c.view(torch.uint8))
         assert torch.equal(p.state_dict()["weight"].view(torch.uint8), c.view(torch.uint8))
+        assert torch.equal(p.kernel_weight()[0], tile_weight(c).view(torch.uint8))
     x = synthetic.activations_outliers(16, K, 5410).cuda()
     before = [p(x) for p in parts]
     merged = FP8Linear.concatenated(parts)
@@ -106,11 +109,18 @@ def test_module_keeps_row_major_state_and_merges():
     y = merged(x)
     for p, b, yy in zip(parts, before, y.split([p.out_features for p in parts], dim=1)):
         assert torch.equal(p(x), b) and torch.equal(yy, b)
-    # a fresh module loaded from the row-major state dict gives the same outputs
+        assert p.tiled_codes.untyped_storage().data_ptr() == merged.tiled_codes.untyped_storage().data_ptr()
+    # a fresh module loaded from the state dict gives the same outputs
     fresh = FP8Linear(K, merged.out_features, device="cuda")
     fresh.load_state_dict(merged.state_dict())
     assert torch.equal(fresh.weight.view(torch.uint8), merged.weight.view(torch.uint8))
     assert torch.equal(fresh(x), y)
+    # the reference's load_codes writes weight in place: the kernels follow
+    with torch.no_grad():
+        parts[1].weight.copy_(codes[2])
+        parts[1].scale.copy_(parts[2].scale)
+    assert torch.equal(parts[1](x), before[2])
+    assert torch.equal(merged(x)[:, 2048:3072], before[2])
     # a part that cannot tile (N % 16 != 0) turns the merge row-major
     odd = FP8Linear(K, 1000, device="cuda")
     odd.load_weight(synthetic.weight(1000, K, 5420).cuda())
@@ -118,7 +128,7 @@ def test_module_keeps_row_major_state_and_merges():
     even.load_weight(synthetic.weight(1024, K, 5421).cuda())
     want = [odd(x), even(x)]
     mixed = FP8Linear.concatenated([odd, even])
-    assert not mixed.tiled and not even.tiled
+    assert not mixed.tiled and not even.tiled and even.tiled_codes is None
     assert torch.equal(odd(x), want[0]) and torch.equal(even(x), want[1])
     assert torch.equal(mixed(x), torch.cat(want, dim=1))
 

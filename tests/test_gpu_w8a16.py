@@ -93,6 +93,31 @@ def test_w8a16_exact_rounding(N, K):
         assert same >= EXACT_EQUAL_MIN, (N, K, M, same)
 
 
+# The FP8 decode kernel's short-tail cases (tests/test_gpu_gemm.py): k ranges
+# whose length leaves 1-3 steps after a wave's full bursts of U steps, with and
+# without split-K.
+SHORT_TAILS = [(7, 16, 6656), (7, 4096, 6656), (16, 96, 6656), (7, 16, 4224), (7, 16, 4608), (7, 4096, 6528),
+               (7, 4096, 5632), (7, 4096, 3968), (7, 4096, 1152), (33, 4096, 6656), (31, 16, 2688), (3, 1040, 2432)]
+
+
+@pytest.mark.parametrize("M,N,K", SHORT_TAILS)
+def test_w8a16_k_ranges_with_short_tails(M, N, K):
+    """The W8A16 decode kernel's guarded last burst of 1-3 steps: the
+    reference's Metal acceptance (>= 99.9% equal to the fp32 math, the float64
+    bound with magnitude 2^-20) and a bitwise-equal second call."""
+    g = torch.Generator().manual_seed(M + N + K)
+    wq, sw = quantize_rows((torch.randn(N, K, generator=g) * 0.02).cuda())
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    y = fp8_matmul_w8a16(x, wq, sw)
+    assert torch.equal(y, fp8_matmul_w8a16(x, wq, sw)), (M, N, K)
+    assert torch.equal(fp8_matmul_w8a16(x, tile_weight(wq), sw, tiled=True), y) if N % 16 == 0 else True
+    out = helpers.bits(y)
+    math = oracle.w8a16_math(helpers.bits(x), helpers.codes_np(wq), sw.cpu().numpy())
+    exact, magnitude = f64_parts(x, wq, sw)
+    assert oracle.bitwise_equal_fraction(out, math) >= MATH_EQUAL_MIN, (M, N, K)
+    assert oracle.within_metal_bound(oracle.bf16_to_f32(out), exact, magnitude * (BOUND_MAGNITUDE / 2.0 ** -20)), (M, N, K)
+
+
 @pytest.mark.parametrize("M", [5, 64, 65, 2048])
 def test_w8a16_large_tiles_and_bias(M):
     """The 256x256 prefill tile (M=2048 over 16384 channels), decode and the
@@ -172,7 +197,7 @@ def test_w8a16_module_mode():
     lin.bias.copy_((torch.randn(N, generator=g) * 0.1).to(torch.bfloat16))
     lin.set_activations("bf16")
     x = torch.randn(3, 5, K, generator=g).to(torch.bfloat16).cuda()
-    assert torch.equal(lin(x), (fp8_matmul_w8a16(x.reshape(-1, K), lin.weight, lin.scale, tiled=lin.tiled) + lin.bias).view(3, 5, N))
+    assert torch.equal(lin(x), (fp8_matmul_w8a16(x.reshape(-1, K), lin.weight, lin.scale) + lin.bias).view(3, 5, N))
     with pytest.raises(ValueError):
         lin.set_lora(torch.zeros(16, K), torch.zeros(N, 16), 1.0)
 
@@ -186,9 +211,9 @@ def test_w8a16_module_mode():
     block = FP8SwiGLU(gate_up, down)
     for M in (4, 100):
         xm = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
-        gu = fp8_matmul_w8a16(xm, gate_up.weight, gate_up.scale, tiled=gate_up.tiled)
+        gu = fp8_matmul_w8a16(xm, gate_up.weight, gate_up.scale)
         h = oracle.swiglu_bf16(helpers.bits(gu[:, :inter]), helpers.bits(gu[:, inter:]))
-        want = fp8_matmul_w8a16(helpers.from_bits(h, "cuda"), down.weight, down.scale, tiled=down.tiled)
+        want = fp8_matmul_w8a16(helpers.from_bits(h, "cuda"), down.weight, down.scale)
         assert torch.equal(block(xm), want)
 
 

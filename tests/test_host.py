@@ -59,13 +59,17 @@ def test_concatenated_parts_become_views():
         assert torch.equal(p.weight.view(torch.uint8), c.view(torch.uint8)) and torch.equal(p.scale, s)
         assert p.weight.untyped_storage().data_ptr() == merged.weight.untyped_storage().data_ptr()
         assert p.scale.untyped_storage().data_ptr() == merged.scale.untyped_storage().data_ptr()
+        assert p.tiled_codes.untyped_storage().data_ptr() == merged.tiled_codes.untyped_storage().data_ptr()
+    from jeeves_amd.fp8 import tile_weight
+    assert torch.equal(merged.kernel_weight()[0], tile_weight(torch.cat(codes)).view(torch.uint8))
 
 
 def test_tiled_layout_on_host():
     """tile_weight's byte order is the C ABI's (fragment of 16 rows x 128 k:
     two 1 KB halves of 64 lanes x 16 bytes, lane = n%16 + 16*((k%128)/32)),
-    untile_weight inverts it, and FP8Linear keeps row-major codes in its state
-    dict while storing them tiled."""
+    untile_weight inverts it, and FP8Linear keeps the reference's row-major
+    codes in ``weight`` (and its state dict) with the kernels' tiled copy in a
+    non-persistent ``tiled_codes`` buffer, rebuilt when ``weight`` changes."""
     from jeeves_amd.fp8 import tile_weight, tileable, untile_weight
 
     g = torch.Generator().manual_seed(3)
@@ -81,12 +85,28 @@ def test_tiled_layout_on_host():
     m = FP8Linear(K, N)
     assert m.tiled
     m.load_codes(codes.view(FP8), torch.ones(N))
-    assert torch.equal(m.weight.view(torch.uint8).view(-1), tiled)
+    assert m.weight.dtype == FP8 and torch.equal(m.weight.view(torch.uint8), codes)
+    w, is_tiled = m.kernel_weight()
+    assert is_tiled and torch.equal(w.view(-1), tiled)
+    assert set(m.state_dict()) == {"weight", "scale"}
     assert torch.equal(m.state_dict()["weight"].view(torch.uint8), codes)
     assert torch.equal(m.codes().view(torch.uint8), codes)
     other = FP8Linear(K, N)
     other.load_state_dict(m.state_dict())
-    assert torch.equal(other.weight.view(torch.uint8), m.weight.view(torch.uint8))
+    assert torch.equal(other.weight.view(torch.uint8), codes)
+    assert torch.equal(other.kernel_weight()[0].view(-1), tiled)
+    # an in-place write to weight (the reference's load_codes does weight.copy_)
+    # is picked up by the next kernel_weight
+    flipped = codes.flip(0).contiguous()
+    with torch.no_grad():
+        m.weight.copy_(flipped.view(FP8))
+    assert torch.equal(m.kernel_weight()[0], tile_weight(flipped))
+    FP8Linear.TILED_COPY = False
+    try:
+        plain = FP8Linear(K, N)
+        assert not plain.tiled and plain.tiled_codes is None and plain.kernel_weight()[0] is plain.weight
+    finally:
+        FP8Linear.TILED_COPY = True
     assert not FP8Linear(K, 1000, device="meta").tiled
 
 

@@ -255,10 +255,36 @@ def test_lora_and_swiglu_closed_forms():
         for n in range(4):
             want = sum(sum(x[m, k] * a[r, k] for k in range(6)) * b[n, r] * 2.0 for r in range(3))
             assert abs(got[m, n] - want) < 1e-12
-    g = oracle.f32_to_bf16(np.array([-3.0, -0.5, 0.0, 0.5, 3.0, 20.0], np.float32))
-    u = oracle.f32_to_bf16(np.array([1.0, 2.0, 3.0, -1.0, 0.25, 1.0], np.float32))
-    want = helpers.bits(torch.nn.functional.silu(helpers.from_bits(g)) * helpers.from_bits(u))
-    assert oracle.bitwise_equal_fraction(oracle.swiglu_bf16(g, u), want) == 1.0
+
+
+def test_swiglu_on_every_bf16_gate_value():
+    """``F.silu(gate) * up`` (model/model.py:583) on all 65536 bf16 gate
+    patterns, against torch's bf16 ops: silu alone (up = 1) and with random
+    bf16 ups of both signs and wide exponent range. NaN results compare by
+    position. (A float64 silu rounded once to bf16 would differ on 17 gates
+    below -88.5, where torch's float32 exp overflows and silu gives -0.)"""
+    g = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    rng = np.random.default_rng(9)
+    ups = [np.full(65536, 0x3F80, np.uint16),
+           oracle.f32_to_bf16((rng.standard_normal(65536) * 2.0 ** rng.integers(-20, 20, 65536)).astype(np.float32))]
+    for u in ups:
+        want = helpers.bits(torch.nn.functional.silu(helpers.from_bits(g)) * helpers.from_bits(u))
+        got = oracle.swiglu_bf16(g, u)
+        assert oracle.bitwise_equal_fraction(got, want) == 1.0
+
+
+def test_add_bias_matches_torch_bf16_add():
+    """FP8Linear.forward's ``y + bias`` (inference/fp8.py:183-184) on bf16:
+    random pairs over a wide exponent range, cancellations, ties and
+    specials, against torch's bf16 add."""
+    rng = np.random.default_rng(10)
+    y = oracle.f32_to_bf16((rng.standard_normal((64, 512)) * 2.0 ** rng.integers(-30, 30, (64, 512))).astype(np.float32))
+    b = oracle.f32_to_bf16((rng.standard_normal(512) * 2.0 ** rng.integers(-30, 30, 512)).astype(np.float32))
+    y[0] = b ^ 0x8000  # exact cancellation
+    y[1] = b  # doubling
+    y[2, :8] = oracle.f32_to_bf16(np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 3e38, 1e-40, 1.0], np.float32))
+    want = helpers.bits(helpers.from_bits(y) + helpers.from_bits(b))
+    assert oracle.bitwise_equal_fraction(oracle.add_bias_bf16(y, b), want) == 1.0
 
 
 def test_acceptance_helpers():
