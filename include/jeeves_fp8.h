@@ -83,8 +83,9 @@ int64_t jv_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t l
  * (inference/fp8.py:183-184) and an optional LoRA adapter
  * (model/lora.py:122-133), as one call:
  *   per-token quantization of x (quantize_rows semantics), then
- *   y[m,n] = bf16( acc[m,n] * sx[m] * w_scale[n] + bias[n]
- *                  + lora_scaling * sum_r (x A^T)[m,r] * B[n,r] ),
+ *   v[m,n] = acc[m,n] * sx[m] * w_scale[n] + lora_scaling * sum_r (x A^T)[m,r] * B[n,r],
+ *   y[m,n] = bf16(v[m,n]), or with a bias bf16( bf16(v[m,n]) + bias[n] )
+ *   (the bias added to the bf16 GEMM output in bf16, as FP8Linear.forward does),
  *   acc[m,n] = sum_k xq[m,k] * w[n,k]  (e4m3 x e4m3, fp32 accumulation).
  * x: [M,K] bf16 (row stride ldx); w: [N,K] e4m3fn (row stride ldw, or
  * ldw = 0: the tiled layout below);
@@ -101,6 +102,28 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
                   const void* lora_a, const void* lora_b, int64_t lora_rank, float lora_scaling, void* y, int64_t ldy,
                   int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, int32_t* tile_counters,
                   int64_t n_counters, void* stream);
+
+/* Bytes of device memory jv_fp8_linear_noalloc keeps per GPU for the rest of
+ * the process (its tile counters and workspace). */
+#define JV_FP8_NOALLOC_SCRATCH_BYTES (16 << 20)
+
+/* jv_fp8_linear without a workspace or tile counters, for callers that cannot
+ * allocate device memory (code under HIP graph capture that must not touch
+ * the allocator, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. It allocates nothing: the quantized
+ * activations, scales, LoRA low-rank activations, split-K partials and tile
+ * counters live in a library-owned device array of
+ * JV_FP8_NOALLOC_SCRATCH_BYTES per GPU (minus 16 KiB of counters for the
+ * workspace: every decode call, M <= 64 and K <= 16384, and prefill batches up
+ * to 4080 tokens at K = 4096 or 1360 at K = 12288 fit). Sizes whose
+ * jv_fp8_linear_workspace_bytes exceed it return JV_ERR_VALUE. Same results
+ * as jv_fp8_linear, bit for bit. Every call on a GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (concurrent streams, or host threads
+ * on one device without ordering) race; calls ordered on one stream do not.
+ * Arguments as jv_fp8_linear. */
+int jv_fp8_linear_noalloc(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
+                          const void* lora_a, const void* lora_b, int64_t lora_rank, float lora_scaling, void* y,
+                          int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* W8A16 parity mode: the arithmetic of the reference's FP8Linear.forward
  * (inference/fp8.py:62-99 with its bias at :183-184, stated as

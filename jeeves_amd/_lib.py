@@ -26,6 +26,8 @@ SIGNATURES: dict[str, tuple] = {
     "jv_fp8_linear": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_float,
                               c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, POINTER(c_int32), c_int64,
                               c_void_p]),
+    "jv_fp8_linear_noalloc": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+                                      c_float, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "jv_fp8_gemm_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64]),
     "jv_fp8_gemm": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
                             c_float, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, POINTER(c_int32), c_int64,

@@ -123,6 +123,52 @@ int check_lora(int64_t rank, const void* a_or_t, const void* b) {
   return JV_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the no-allocation entry point (jv_fp8_linear_noalloc): one
+// file-scope device array per GPU the library runs on, held until the process
+// ends -- the tile counters first, then jv_fp8_linear's workspace. In host code
+// `scratch` is only a stand-in for the symbol; its device address comes from
+// hipGetSymbolAddress, once per device with that device current, and only that
+// address is handed to kernels.
+constexpr int64_t kNoAllocCounterSlots = 4096;
+constexpr int64_t kNoAllocCounterBytes = kNoAllocCounterSlots * 4;
+constexpr int64_t kNoAllocWorkspaceBytes = JV_FP8_NOALLOC_SCRATCH_BYTES - kNoAllocCounterBytes;
+static_assert(kNoAllocCounterBytes % 256 == 0, "workspace alignment");
+static __device__ __align__(256) uint8_t scratch[JV_FP8_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+std::atomic<uint8_t*> g_scratch[kMaxDevices];
+
+__global__ void zero_words(int32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// The calling thread's current device's scratch address; on the first call on
+// a device, also clears its tile counters (a fill kernel on `stream`, which
+// orders it before the GEMM that follows on the same stream).
+int scratch_of_current_device(hipStream_t stream, uint8_t** out) {
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices)
+    return fail(JV_ERR_HIP, "cannot query the current HIP device");
+  uint8_t* p = g_scratch[device].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[device].load(std::memory_order_relaxed);
+    if (!p) {
+      if (int rc = hip_status(hipGetSymbolAddress(reinterpret_cast<void**>(&p), HIP_SYMBOL(scratch)),
+                              "no-allocation scratch address"))
+        return rc;
+      zero_words<<<dim3((unsigned)(kNoAllocCounterSlots / 256)), dim3(256), 0, stream>>>(reinterpret_cast<int32_t*>(p),
+                                                                                     (int)kNoAllocCounterSlots);
+      if (int rc = hip_status(hipGetLastError(), "no-allocation scratch clear")) return rc;
+      g_scratch[device].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return JV_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -309,6 +355,26 @@ int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count) {
   if (K <= 0 || N <= 0 || cu_count <= 0 || !jv::decode_kernel_for(M, N, cu_count)) return 0;
   const jv::DecodePlan p = jv::decode_plan(M, N, K, cu_count);
   return p.splits > 1 ? p.groups : 0;
+}
+
+int jv_fp8_linear_noalloc(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
+                          const void* lora_a, const void* lora_b, int64_t lora_rank, float lora_scaling, void* y,
+                          int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
+  if (int rc = check_gemm_shape(M, N, K)) return rc;
+  if (int rc = check_lora(lora_rank, lora_a, lora_b)) return rc;
+  if (M == 0) return JV_OK;
+  const int64_t need = jv_fp8_linear_workspace_bytes(M, N, K, lora_rank);
+  if (need < 0) return fail(JV_ERR_HIP, "cannot query the device's compute units");
+  if (need > kNoAllocWorkspaceBytes)
+    return fail(JV_ERR_VALUE,
+                "jv_fp8_linear_noalloc: M=%lld N=%lld K=%lld needs %lld bytes of scratch, more than its %lld; call "
+                "jv_fp8_linear with a workspace instead",
+                (long long)M, (long long)N, (long long)K, (long long)need, (long long)kNoAllocWorkspaceBytes);
+  uint8_t* base = nullptr;
+  if (int rc = scratch_of_current_device((hipStream_t)stream, &base)) return rc;
+  return jv_fp8_linear(x, ldx, w, ldw, w_scale, bias, lora_a, lora_b, lora_rank, lora_scaling, y, ldy, M, N, K,
+                       base + kNoAllocCounterBytes, kNoAllocWorkspaceBytes, reinterpret_cast<int32_t*>(base),
+                       kNoAllocCounterSlots, stream);
 }
 
 }  // extern "C"
