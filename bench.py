@@ -1,32 +1,42 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X FP8 linear path on one GPU.
 
-A step is one pass of the decode workload: the six 9B-class projections
-(q, k, v: 4096->4096/1024/1024, o: 4096->4096, fused gate+up: 4096->24576,
-down: 12288->4096) each applied once to M = 16 tokens through the full path
-(per-token e4m3 quantization of the bf16 activations + FP8 x FP8 GEMM + scale
-epilogue -> bf16). As in the reference engine, which replays its decode passes
-as CUDA graphs (inference/engine.py:351-360), each step is a captured HIP graph
-replay, so host launch overhead is not measured. Weights rotate over enough
+A step is one decoder layer's FP8 linears at M = 16 decode tokens, run the way
+the reference engine runs them: q, k and v merged into one projection
+(4096 -> 6144, inference/engine.py:154-165, :272-284), o (4096 -> 4096), the
+gate+up (4096 -> 24576) as one GEMM with SwiGLU in its epilogue, the down
+projection's quantization of h, and down (12288 -> 4096). Each distinct input is
+quantized once (four per-token e4m3 quantizer launches), every GEMM applies the
+scale epilogue -> bf16. As in the reference engine, which replays its decode
+passes as CUDA graphs (inference/engine.py:351-360), each step is a captured
+HIP graph replay. Weights are in FP8Linear's tiled layout and rotate over enough
 copies (>= 512 MB) that every step reads them from HBM, not the 256 MB
 Infinity Cache. Inputs are resident in HBM before timing starts.
 
-value        algorithmic bytes of the six linears / step time (GB/s), with
+value        algorithmic bytes of the layer's linears / step time (GB/s), with
              bytes per linear = N*K (e4m3 W) + 4N (scales) + 2MK (bf16 x) + 2MN (bf16 y)
-roofline     the dominant kernel (the fused gate+up decode GEMM) alone: a graph
-             of back-to-back launches on rotated weights, timed with HIP events
-             on its stream; algorithmic bytes / average launch time vs 8 TB/s
-prefill      the same six projections at M = 2048 (TFLOP/s, 2*M*N*K per
-             linear), with the gate+up prefill GEMM's roofline vs 5.0 PFLOP/s
+roofline     the dominant kernel (the gate+up decode GEMM) alone: graphs of
+             back-to-back launches on rotated weights, timed with HIP events
+             on their stream; algorithmic bytes / average launch time vs
+             8 TB/s; `traffic` is copied from the committed rocprofv3 PMC
+             summary (profiles/), not measured in this run
+decode       the layer step, the six separate projections each with its own
+             quantizer (q, k, v, o, gate+up, down), per-kernel GEMM times at
+             M = 16 including the merged q/k/v, and per-kernel GEMM times at
+             M = 1, 4, 32 (the other decode batch sizes) and 64, 96, 128 (the
+             engine's decode row counts, inference/engine.py:299-306)
+prefill      the same layer and the six projections at M = 2048 (TFLOP/s,
+             2*M*N*K per linear), per-kernel times at M = 512, 2048, 8192, and
+             the gate+up prefill GEMM's roofline vs 5.0 PFLOP/s
 workloads    the decoder layer's linear stack at M = 512 with a rank-16 LoRA
-             on every projection, the ragged request mix (64 log-uniform
-             sequence lengths packed into one batch through 32 layers of
-             random weights, then 64 decode steps at batch 64), and the
-             lm_head (248320 x 4096) at M = 1 and 16: time, TFLOP/s or GB/s
-             and roofline fraction per phase
-cpu_baseline the CPU oracle's dequantize-then-matmul (numpy float32, BLAS
-             threads) on the same decode step, timed on the host for a bounded
-             number of steps
+             on every projection (q, k, v separate: each has its own adapter),
+             the ragged request mix (64 log-uniform sequence lengths packed
+             into one batch through 32 layers of random weights, then 64
+             decode steps at batch 64), and the lm_head (248320 x 4096) at
+             M = 1 and 16: time, TFLOP/s or GB/s and roofline fraction
+cpu_baseline the CPU oracle's quantize + dequantize-then-matmul (numpy float32,
+             BLAS threads) on the same decode layer step for a bounded number
+             of steps, and the single linear (16 x 4096 -> 4096) on its own
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -36,6 +46,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 from pathlib import Path
@@ -48,12 +59,18 @@ HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 ROTATE_BYTES = 512 << 20
 LAUNCHES_PER_GRAPH = 24
+# Decode batch sizes besides 16: the other decode rows of the decode workload,
+# then the engine's decode row counts above 64 (4B, 12B and 16B tokens rounded
+# to a power of two, inference/engine.py:299-306).
+DECODE_SWEEP_ROWS = (1, 4, 32, 64, 96, 128)
+PREFILL_SWEEP_ROWS = (512, 8192)
+PMC_SUMMARY = "profiles/gate_up_hbm_traffic_pmc.md"
 
 
 def measured_traffic(key: str):
-    """HBM bytes per launch measured with rocprofv3 PMC counters, from the
-    committed summary (None when absent)."""
-    path = ROOT / "profiles" / "gate_up_hbm_traffic_pmc.md"
+    """HBM bytes per launch measured with rocprofv3 PMC counters, copied from
+    the committed summary (None when absent)."""
+    path = ROOT / PMC_SUMMARY
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -106,22 +123,43 @@ class Bench:
         return start.elapsed_time(end) / replays
 
 
-def build_set(torch, synthetic, quantize_rows, M: int, case):
-    """Quantized weights (rotated copies) and bf16 activations for one
-    workload. The codes are stored as FP8Linear stores them for these shapes:
-    in the tiled layout (tile_weight)."""
+def layer_shapes(synthetic) -> dict[str, tuple[int, int]]:
+    """(N, K) of the layer's linears as the engine holds them: q/k/v merged."""
+    s = synthetic.SHAPES
+    return {"qkv": (s["q"][0] + s["k"][0] + s["v"][0], s["q"][1]), "o": s["o"], "gate_up": s["gate_up"], "down": s["down"]}
+
+
+def make_weights(torch, synthetic, quantize_rows) -> dict:
+    """Tiled e4m3 codes and scales of the six projections (the decode and
+    prefill workloads' weights), plus q/k/v merged the way FP8Linear.concatenated
+    merges them (whole 16-row tiles: the merged tiled copy is the parts' copies
+    one after another)."""
     from jeeves_amd.fp8 import tile_weight
 
-    weights, xs = {}, {}
+    w = {}
     for name in synthetic.SHAPES:
-        x, w = case(name, M)
-        wq, sw = quantize_rows(w.cuda())
-        weights[name] = (tile_weight(wq), sw)
-        xs[name] = x.cuda()
-    per_copy = sum(wq.numel() for wq, _ in weights.values())
-    copies = max(2, -(-ROTATE_BYTES // per_copy) + 1)
-    rot = [weights] + [{n: (wq.clone(), sw.clone()) for n, (wq, sw) in weights.items()} for _ in range(copies - 1)]
-    return rot, xs, copies, per_copy
+        wq, sw = quantize_rows(synthetic.decode_case(name, 1)[1].cuda())
+        w[name] = (tile_weight(wq), sw)
+    w["qkv"] = (torch.cat([w[n][0] for n in ("q", "k", "v")]), torch.cat([w[n][1] for n in ("q", "k", "v")]))
+    return w
+
+
+class Rotation:
+    """Copies of each weight totalling at least ROTATE_BYTES, so back-to-back
+    launches read their weights from HBM rather than the Infinity Cache."""
+
+    def __init__(self, weights):
+        self.weights, self.cache = weights, {}
+
+    def copies(self, name: str):
+        if name not in self.cache:
+            wq, sw = self.weights[name]
+            n = max(2, -(-ROTATE_BYTES // wq.numel()) + 1)
+            self.cache[name] = [(wq, sw)] + [(wq.clone(), sw) for _ in range(n - 1)]
+        return self.cache[name]
+
+    def drop(self):
+        self.cache.clear()
 
 
 def quantized_operands(torch, fp8, x):
@@ -137,54 +175,198 @@ def quantized_operands(torch, fp8, x):
     return codes, sx, M
 
 
-def kernel_ms(b: Bench, fp8, rot, operands, name: str, replays: int) -> float:
-    """Average time (ms) of one GEMM kernel launch for projection `name` on the
-    activation codes fp8_matmul would produce, from graphs of back-to-back
-    launches on the bench stream. The launches rotate over copies of this
-    projection's weights totalling at least ROTATE_BYTES, so each launch reads
-    its weights from HBM rather than the Infinity Cache."""
+def kernel_ms(b: Bench, fp8, copies, operands, replays: int, graphs: int = 4) -> float:
+    """Average time (ms) of one GEMM kernel launch on the activation codes
+    fp8_matmul would produce, from graphs of back-to-back launches on the bench
+    stream over rotated weight copies."""
     xq, sx, packed_rows = operands
-    wq0, sw0 = rot[0][name]
-    n_copies = max(2, -(-ROTATE_BYTES // wq0.numel()) + 1)
-    copies = [(wq0, sw0)] + [(wq0.clone(), sw0) for _ in range(n_copies - 1)]
-    graphs = []
-    for c in range(min(len(copies), 4)):
+    gs = []
+    for c in range(min(len(copies), graphs)):
         def launches(c=c):
             for j in range(LAUNCHES_PER_GRAPH):
                 wq, sw = copies[(c * LAUNCHES_PER_GRAPH + j) % len(copies)]
                 fp8.fp8_matmul_quantized(xq, sx, wq, sw, packed_rows=packed_rows, tiled=True)
-        graphs.append(b.capture(launches))
-    ms = b.time_graphs(graphs, replays, 3) / LAUNCHES_PER_GRAPH
-    del graphs, copies
+        gs.append(b.capture(launches))
+    ms = b.time_graphs(gs, replays, 3) / LAUNCHES_PER_GRAPH
+    del gs
     return ms
 
 
+def layer_inputs(synthetic, M: int, K: int, case) -> dict:
+    """Distinct bf16 inputs of the layer's linears: the attention input (for
+    q/k/v), the attention output (o) and the MLP input (gate+up)."""
+    x = case("q", M)[0]
+    g = synthetic.gen(900 + M)
+    import torch
+
+    return {"attn": x, "o": x[:, torch.randperm(K, generator=g)].contiguous(),
+            "mlp": x[:, torch.randperm(K, generator=g)].contiguous()}
+
+
+def layer_linears(fp8, synthetic, xs, weights, lora=None):
+    """One decoder layer's linear stack. With `xs` a dict (attention input,
+    attention output, MLP input) and merged q/k/v weights: the engine's merged
+    qkv projection, o, gate+up with SwiGLU in its epilogue (h), the down
+    projection's quantization of h, down. With `xs` one tensor: q, k, v
+    (separate, each with its own LoRA adapter when `lora` is given), o and
+    gate+up all on it, then the same SwiGLU and down."""
+    if isinstance(xs, dict):
+        wq, sw = weights["qkv"]
+        fp8.fp8_matmul(xs["attn"], wq, sw, tiled=True)
+        wq, sw = weights["o"]
+        fp8.fp8_matmul(xs["o"], wq, sw, tiled=True)
+        h = xs["mlp"]
+    else:
+        h = xs
+        for name in ("q", "k", "v", "o"):
+            wq, sw = weights[name]
+            fp8.fp8_matmul(h, wq, sw, tiled=True, lora=lora[name] if lora else None)
+    wq, sw = weights["gate_up"]
+    hh = fp8.gate_up_swiglu(h, wq, sw, tiled=True, lora=lora["gate_up"] if lora else None)
+    res = fp8.quantize_swiglu_output(hh, lora_a=lora["down"][0] if lora else None, packed=True)
+    wq, sw = weights["down"]
+    return fp8.fp8_matmul_quantized(res[0], res[1], wq, sw, lora_t=res[2] if lora else None,
+                                    lora_b=lora["down"][1] if lora else None,
+                                    lora_scaling=lora["down"][2] if lora else 0.0, packed_rows=h.shape[0], tiled=True)
+
+
+def layer_bytes(synthetic, M: int) -> int:
+    return sum(linear_bytes(M, N, K) for N, K in layer_shapes(synthetic).values())
+
+
+def layer_flops(synthetic, M: int, rank: int = 0) -> int:
+    return sum(2 * M * N * K + 2 * M * rank * (K + N) for N, K in synthetic.SHAPES.values())
+
+
+def layer_step_ms(b: Bench, torch, fp8, synthetic, weights, xs, replays: int, warmup: int) -> tuple[float, int]:
+    """ms per layer step (HIP graph replay) over rotated copies of the layer's
+    weights, and the number of copies."""
+    names = tuple(layer_shapes(synthetic))
+    per_copy = sum(weights[n][0].numel() for n in names)
+    n = max(2, -(-ROTATE_BYTES // per_copy) + 1)
+    sets = [{k: weights[k] for k in names}] + [{k: (weights[k][0].clone(), weights[k][1]) for k in names}
+                                               for _ in range(n - 1)]
+    graphs = [b.capture(lambda s=s: layer_linears(fp8, synthetic, xs, s)) for s in sets]
+    ms = b.time_graphs(graphs, replays, warmup)
+    del graphs, sets
+    torch.cuda.empty_cache()
+    return ms, n
+
+
+def six_step_ms(b: Bench, torch, fp8, synthetic, weights, case, M: int, replays: int, warmup: int) -> float:
+    """ms per step of the six separate projections (q, k, v, o, gate+up, down),
+    each quantizing its own input, over rotated weight copies."""
+    names = tuple(synthetic.SHAPES)
+    xs = {name: case(name, M)[0].cuda() for name in names}
+    per_copy = sum(weights[n][0].numel() for n in names)
+    n = max(2, -(-ROTATE_BYTES // per_copy) + 1)
+    sets = [{k: weights[k] for k in names}] + [{k: (weights[k][0].clone(), weights[k][1]) for k in names}
+                                               for _ in range(n - 1)]
+
+    def step(s):
+        for name in names:
+            fp8.fp8_matmul(xs[name], s[name][0], s[name][1], tiled=True)
+
+    graphs = [b.capture(lambda s=s: step(s)) for s in sets]
+    ms = b.time_graphs(graphs, replays, warmup)
+    del graphs, sets
+    torch.cuda.empty_cache()
+    return ms
+
+
+def per_kernel(b, torch, fp8, synthetic, rot, M: int, case, replays: int, bound: str) -> dict:
+    """GEMM kernel time per projection at M tokens (and the merged q/k/v), with
+    GB/s or TFLOP/s and the fraction of the bound's peak."""
+    out = {}
+    shapes = dict(synthetic.SHAPES, **{"qkv": layer_shapes(synthetic)["qkv"]})
+    for name, (N, K) in shapes.items():
+        x = case("q" if name == "qkv" else name, M)[0].cuda()
+        ms = kernel_ms(b, fp8, rot.copies(name), quantized_operands(torch, fp8, x), replays)
+        if bound == "hbm":
+            gbs = linear_bytes(M, N, K) / (ms * 1e-3) / 1e9
+            out[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        else:
+            tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+            out[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
+    return out
+
+
+def host_description() -> dict:
+    model = platform.processor() or ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    import numpy
+    import torch
+
+    return {"cpu_model": model, "host_cores": os.cpu_count(), "torch": torch.__version__, "numpy": numpy.__version__}
+
+
+def cpu_threads() -> int:
+    """BLAS threads for the CPU baseline: the cores this process may run on,
+    capped by OMP_NUM_THREADS when the environment sets it (the GPU box gives
+    each GPU's jobs a share of its cores and says so there)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(n, 1)
+
+
 def cpu_baseline(synthetic, M: int, budget_s: float) -> dict:
+    """The oracle on the host: per-token quantization of x, per-call weight
+    dequantization, float32 sgemm (numpy BLAS), scale epilogue, bf16 rounding.
+    The decode layer step (the four linears of the GPU step, q/k/v merged) for
+    up to `budget_s` seconds, then the single linear (16 x 4096 -> 4096) alone."""
+    import numpy as np
     from threadpoolctl import threadpool_limits
 
     import oracle
 
-    cores = min(os.cpu_count() or 1, 16)
+    threads = cpu_threads()
+    shapes = layer_shapes(synthetic)
     ops = []
-    total_bytes = 0
-    for name, (N, K) in synthetic.SHAPES.items():
-        x, w = synthetic.decode_case(name, M)
-        wq, sw = oracle.quantize_rows(w.float().numpy())
-        ops.append((x.float().numpy(), wq, sw))
-        total_bytes += linear_bytes(M, N, K)
-    with threadpool_limits(limits=cores):
+    for i, (name, (N, K)) in enumerate(shapes.items()):
+        x = synthetic.activations_outliers(M, K, 950 + i).float().numpy()
+        w = synthetic.weight(N, K, 960 + i).float().numpy()
+        ops.append((x, *oracle.quantize_rows(w)))
+    step_bytes = layer_bytes(synthetic, M)
+
+    def linear(xf, wq, sw):
+        xq, sx = oracle.quantize_rows(xf)
+        return oracle.f32_to_bf16(oracle.dequant_matmul_f32(xq, sx, wq, sw))
+
+    with threadpool_limits(limits=threads):
+        for op in ops:  # warm-up: BLAS thread pool and page faults
+            linear(*op)
         steps, t0 = 0, time.perf_counter()
         while True:
-            for xf, wq, sw in ops:
-                xq, sx = oracle.quantize_rows(xf)
-                oracle.f32_to_bf16(oracle.dequant_matmul_f32(xq, sx, wq, sw))
+            for op in ops:
+                linear(*op)
             steps += 1
             elapsed = time.perf_counter() - t0
             if elapsed >= budget_s or steps >= 50:
                 break
-    return {"value": round(total_bytes * steps / elapsed / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"{steps} decode steps (M={M}, the six projections: per-token quant, per-call weight dequant, "
-                      f"float32 sgemm, bf16 rounding) in {elapsed:.1f} s"}
+        x1, w1 = synthetic.single_linear()
+        op1 = (x1.float().numpy(), *oracle.quantize_rows(w1.float().numpy()))
+        linear(*op1)
+        times = []
+        for _ in range(7):
+            t = time.perf_counter()
+            linear(*op1)
+            times.append(time.perf_counter() - t)
+        single_ms = float(np.median(times)) * 1e3
+    return {"value": round(step_bytes * steps / elapsed / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} decode layer steps (M={M}; q/k/v merged, o, gate+up, down: per-token quant, per-call "
+                      f"weight dequant, float32 sgemm, bf16 rounding) in {elapsed:.1f} s on {threads} BLAS threads",
+            "single_linear_16x4096x4096": {"ms": round(single_ms, 3),
+                                           "GB/s": round(linear_bytes(16, 4096, 4096) / (single_ms * 1e-3) / 1e9, 4),
+                                           "note": "median of 7 calls, same pipeline"},
+            **host_description()}
 
 
 def pmc_driver(torch, fp8, synthetic, quantize_rows, launches: int = 10) -> None:
@@ -217,27 +399,6 @@ def device_weight(torch, synthetic, N: int, K: int, seed: int):
     return (torch.randn(N, K, device="cuda", generator=g) * synthetic.WEIGHT_STD).to(torch.bfloat16)
 
 
-def layer_linears(fp8, synthetic, h, weights, lora=None):
-    """One decoder layer's linear stack on h: q, k, v, o and gate+up, SwiGLU
-    fused with the down projection's activation quantization, down (the same
-    input feeds every projection: only the linear layers are timed)."""
-    for name in ("q", "k", "v", "o"):
-        wq, sw = weights[name]
-        fp8.fp8_matmul(h, wq, sw, tiled=True, lora=lora[name] if lora else None)
-    wq, sw = weights["gate_up"]
-    gu = fp8.fp8_matmul(h, wq, sw, tiled=True, lora=lora["gate_up"] if lora else None)
-    inter = synthetic.INTERMEDIATE
-    res = fp8.swiglu_quantize(gu[:, :inter], gu[:, inter:], lora_a=lora["down"][0] if lora else None, packed=True)
-    wq, sw = weights["down"]
-    return fp8.fp8_matmul_quantized(res[0], res[1], wq, sw, lora_t=res[2] if lora else None,
-                                    lora_b=lora["down"][1] if lora else None,
-                                    lora_scaling=lora["down"][2] if lora else 0.0, packed_rows=h.shape[0], tiled=True)
-
-
-def layer_flops(synthetic, M: int, rank: int = 0) -> int:
-    return sum(2 * M * N * K + 2 * M * rank * (K + N) for N, K in synthetic.SHAPES.values())
-
-
 def workloads(torch, b: Bench, fp8, synthetic, quantize_rows) -> dict:
     """The decoder layer with LoRA at M = 512 and the ragged request mix through
     32 layers (prefill of the packed batch, then 64 decode steps at batch 64):
@@ -261,34 +422,40 @@ def workloads(torch, b: Bench, fp8, synthetic, quantize_rows) -> dict:
     fl = layer_flops(synthetic, M, synthetic.LORA_RANK)
     tf = fl / (ms * 1e-3) / 1e12
     out["decoder_layer_lora_m512"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
-                                      "flops": fl, "note": "q, k, v, o, gate+up, SwiGLU-quant, down with rank-16 LoRA each; "
+                                      "flops": fl, "note": "q, k, v, o, gate+up with SwiGLU in its epilogue, quantization of h, down, rank-16 LoRA on each; "
                                                            "HIP graph replay over 4 weight copies (772 MB)"}
     del graphs, copies
     torch.cuda.empty_cache()
     log(f"bench: decoder layer (LoRA, M=512) {ms * 1e3:.1f} us, {tf:.0f} TFLOP/s")
 
-    # ragged mix: 32 layers of random weights (6.2 GB of e4m3 codes)
+    # ragged mix: 32 layers of random weights (6.2 GB of e4m3 codes), q/k/v merged as the engine merges them
     layers = []
     for layer in range(32):
-        weights = {}
+        w = {}
         for i, (name, (N, K)) in enumerate(synthetic.SHAPES.items()):
             wq, sw = quantize_rows(device_weight(torch, synthetic, N, K, 700 + 10 * layer + i))
-            weights[name] = (fp8.tile_weight(wq), sw)
-        layers.append(weights)
+            w[name] = (fp8.tile_weight(wq), sw)
+        w["qkv"] = (torch.cat([w[n][0] for n in ("q", "k", "v")]), torch.cat([w[n][1] for n in ("q", "k", "v")]))
+        for n in ("q", "k", "v"):
+            del w[n]
+        layers.append(w)
     torch.cuda.empty_cache()
     lengths = synthetic.ragged_lengths()
     h = torch.cat([synthetic.activations_heavy_tail(n, synthetic.HIDDEN, 5000 + i) for i, n in enumerate(lengths)]).cuda()
     T = h.shape[0]
+    g = torch.Generator().manual_seed(5001)
+    xs = {"attn": h, "o": h[:, torch.randperm(synthetic.HIDDEN, generator=g).cuda()].contiguous(),
+          "mlp": h[:, torch.randperm(synthetic.HIDDEN, generator=g).cuda()].contiguous()}
     with torch.cuda.stream(b.stream):
-        for weights in layers[:2]:
-            layer_linears(fp8, synthetic, h, weights)
+        for w in layers[:2]:
+            layer_linears(fp8, synthetic, xs, w)
         b.stream.synchronize()
         best = None
         for _ in range(2):
             st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             st.record(b.stream)
-            for weights in layers:
-                layer_linears(fp8, synthetic, h, weights)
+            for w in layers:
+                layer_linears(fp8, synthetic, xs, w)
             en.record(b.stream)
             en.synchronize()
             t = st.elapsed_time(en)
@@ -296,17 +463,20 @@ def workloads(torch, b: Bench, fp8, synthetic, quantize_rows) -> dict:
     pre_ms = best
     pre_fl = 32 * layer_flops(synthetic, T)
     pre_tf = pre_fl / (pre_ms * 1e-3) / 1e12
-    del h
+    del h, xs
     torch.cuda.empty_cache()
     xd = synthetic.activations_outliers(64, synthetic.HIDDEN, 5500).cuda()
+    g = torch.Generator().manual_seed(5501)
+    xds = {"attn": xd, "o": xd[:, torch.randperm(synthetic.HIDDEN, generator=g).cuda()].contiguous(),
+           "mlp": xd[:, torch.randperm(synthetic.HIDDEN, generator=g).cuda()].contiguous()}
 
     def decode_step():
-        for weights in layers:
-            layer_linears(fp8, synthetic, xd, weights)
+        for w in layers:
+            layer_linears(fp8, synthetic, xds, w)
 
-    g = b.capture(decode_step)
-    step_ms = b.time_graphs([g], 64, 2)
-    dec_bytes = 32 * sum(linear_bytes(64, N, K) for N, K in synthetic.SHAPES.values())
+    graph = b.capture(decode_step)
+    step_ms = b.time_graphs([graph], 64, 2)
+    dec_bytes = 32 * layer_bytes(synthetic, 64)
     dec_gbs = dec_bytes / (step_ms * 1e-3) / 1e9
     out["ragged_32_layers"] = {
         "tokens_prefill": T, "sequences": len(lengths),
@@ -316,12 +486,12 @@ def workloads(torch, b: Bench, fp8, synthetic, quantize_rows) -> dict:
         "decode_us_per_step": round(step_ms * 1e3, 1), "decode_GB/s": round(dec_gbs, 1),
         "decode_frac_of_hbm_peak": round(dec_gbs / HBM_PEAK_GBS, 4),
         "linear_ms_total": round(pre_ms + 64 * step_ms, 3),
-        "note": "linear layers only (q, k, v, o, gate+up, SwiGLU-quant, down per layer, no LoRA), random-init "
+        "note": "linear layers only (q/k/v merged, o, gate+up with SwiGLU epilogue, quantization of h, down per layer, no LoRA), random-init "
                 "weights; prefill eager on the packed batch, each decode step one HIP graph of 32 layers",
     }
     log(f"bench: ragged prefill {T} tokens {pre_ms:.2f} ms ({pre_tf:.0f} TFLOP/s), decode step {step_ms * 1e3:.0f} us "
         f"({dec_gbs:.0f} GB/s)")
-    del g, layers
+    del graph, layers
     torch.cuda.empty_cache()
 
     # lm_head, N = 248320 x K = 4096 (inference/engine.py:293-297): 1.02 GB of tiled e4m3 codes, more
@@ -356,8 +526,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the per-kernel lines at the other batch sizes")
     ap.add_argument("--no-workloads", action="store_true",
-                    help="skip the decoder-layer (LoRA, M=512) and 32-layer ragged-mix measurements")
+                    help="skip the decoder-layer (LoRA, M=512), 32-layer ragged-mix and lm_head measurements")
     ap.add_argument("--pmc-driver", action="store_true",
                     help="run only the hardware-counter workload (copy calibration + gate+up GEMMs), no timing")
     args = ap.parse_args()
@@ -381,28 +552,31 @@ def main() -> int:
     dev_name = torch.cuda.get_device_name(0)
     M = args.rows
     log(f"bench: decode M={M} on {dev_name}")
-    rot, xs, copies, per_copy = build_set(torch, synthetic, quantize_rows, M, synthetic.decode_case)
-    step_bytes = sum(linear_bytes(M, *synthetic.SHAPES[n]) for n in synthetic.SHAPES)
+    weights = make_weights(torch, synthetic, quantize_rows)
+    rot = Rotation(weights)
+    K = synthetic.HIDDEN
 
-    def step(c):
-        for name in synthetic.SHAPES:
-            wq, sw = rot[c][name]
-            fp8.fp8_matmul(xs[name], wq, sw, tiled=True)
-
-    graphs = [b.capture(lambda c=c: step(c)) for c in range(copies)]
-    ms = b.time_graphs(graphs, args.steps, args.warmup)
+    # the headline: one decoder layer's linears, engine-style
+    xs = {k: v.cuda() for k, v in layer_inputs(synthetic, M, K, synthetic.decode_case).items()}
+    ms, n_sets = layer_step_ms(b, torch, fp8, synthetic, weights, xs, args.steps, args.warmup)
+    step_bytes = layer_bytes(synthetic, M)
     value = step_bytes / (ms * 1e-3) / 1e9
-    log(f"bench: decode step {ms * 1e3:.1f} us, {value:.0f} GB/s")
+    log(f"bench: decode layer step {ms * 1e3:.1f} us, {value:.0f} GB/s")
+    six_ms = six_step_ms(b, torch, fp8, synthetic, weights, synthetic.decode_case, M, max(args.steps // 2, 20), 5)
+    six_bytes = sum(linear_bytes(M, *synthetic.SHAPES[n]) for n in synthetic.SHAPES)
+    log(f"bench: six-projection step {six_ms * 1e3:.1f} us")
 
-    per_shape = {}
-    for name, (n_, k_) in synthetic.SHAPES.items():
-        t = kernel_ms(b, fp8, rot, quantized_operands(torch, fp8, xs[name]), name, 40)
-        per_shape[name] = {"us": round(t * 1e3, 2), "GB/s": round(linear_bytes(M, n_, k_) / (t * 1e-3) / 1e9, 1)}
-    N, K = synthetic.SHAPES["gate_up"]
-    k_ms = per_shape["gate_up"]["us"] * 1e-3
-    k_bytes = linear_bytes(M, N, K)
+    kernels = per_kernel(b, torch, fp8, synthetic, rot, M, synthetic.decode_case, 40, "hbm")
+    N, Kg = synthetic.SHAPES["gate_up"]
+    k_ms = kernels["gate_up"]["us"] * 1e-3
+    k_bytes = linear_bytes(M, N, Kg)
     k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
-    log(f"bench: decode GEMM kernels {per_shape}")
+    log(f"bench: decode GEMM kernels {kernels}")
+    sweep = {}
+    if not args.no_sweep:
+        for m in DECODE_SWEEP_ROWS:
+            sweep[f"m{m}"] = per_kernel(b, torch, fp8, synthetic, rot, m, synthetic.decode_case, 16, "hbm")
+        log(f"bench: decode sweep done ({', '.join(sweep)})")
 
     result = {
         "metric": METRIC,
@@ -418,51 +592,62 @@ def main() -> int:
         "dtype": "fp8_e4m3 (fp32 accumulate)",
         "data": "synthetic (seeded random-init weights and activations)",
         "config": {
-            "workload": f"decode M={M}: 9B-class FP8 linears q 4096->4096, k/v 4096->1024, o 4096->4096, gate+up "
-                        f"4096->24576, down 12288->4096, one pass each per step (quant + GEMM + epilogue) replayed as "
-                        f"a HIP graph, weights in FP8Linear's tiled layout rotated over {copies} copies "
-                        f"({copies * per_copy / 2**20:.0f} MiB)",
+            "workload": f"decode M={M}: one 9B-class decoder layer's FP8 linears as the reference engine runs them: "
+                        f"q/k/v merged 4096->6144, o 4096->4096, gate+up 4096->24576 with SwiGLU in its GEMM "
+                        f"epilogue, down 12288->4096; each distinct input quantized once (4 quantizer + 4 GEMM "
+                        f"launches), HIP graph replay, weights in FP8Linear's tiled layout rotated over {n_sets} copies",
             "tokens": M,
             "device": dev_name,
         },
         "roofline": {"bound": "hbm", "kernel": "gemm_decode_kernel (gate+up, N=24576 K=4096, M=16)",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(f"decode_gate_up_m{M}"), "avg_launch_us": round(k_ms * 1e3, 3),
-                     "bytes_per_launch": k_bytes},
-        "decode_kernels": per_shape,
+                     "traffic": measured_traffic(f"decode_gate_up_m{M}"),
+                     "traffic_source": f"copied from {PMC_SUMMARY} (rocprofv3 PMC FETCH_SIZE + WRITE_SIZE), not measured "
+                                       "in this run",
+                     "avg_launch_us": round(k_ms * 1e3, 3), "bytes_per_launch": k_bytes},
+        "decode": {
+            "layer_step": {"us": round(ms * 1e3, 2), "GB/s": round(value, 1), "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+                           "bytes": step_bytes},
+            "six_projections_step": {"us": round(six_ms * 1e3, 2),
+                                     "GB/s": round(six_bytes / (six_ms * 1e-3) / 1e9, 1),
+                                     "note": "q, k, v, o, gate+up, down each with its own quantizer launch"},
+            "kernels_m16": kernels,
+            "kernels_sweep": sweep,
+        },
     }
 
     if not args.no_prefill:
         Mp = args.prefill_rows
         log(f"bench: prefill M={Mp}")
-        del rot, graphs
-        torch.cuda.empty_cache()
-        prot, pxs, pcopies, _ = build_set(torch, synthetic, quantize_rows, Mp, synthetic.prefill_case)
-        flops = sum(2 * Mp * n_ * k_ for n_, k_ in synthetic.SHAPES.values())
-
-        def pstep(c):
-            for name in synthetic.SHAPES:
-                wq, sw = prot[c][name]
-                fp8.fp8_matmul(pxs[name], wq, sw, tiled=True)
-
-        pgraphs = [b.capture(lambda c=c: pstep(c)) for c in range(pcopies)]
-        pms = b.time_graphs(pgraphs, max(args.steps // 8, 20), 3)
-        pshape = {}
-        for name, (n_, k_) in synthetic.SHAPES.items():
-            t = kernel_ms(b, fp8, prot, quantized_operands(torch, fp8, pxs[name]), name, 8)
-            pshape[name] = {"us": round(t * 1e3, 2), "TFLOP/s": round(2 * Mp * n_ * k_ / (t * 1e-3) / 1e12, 1)}
-        pk = pshape["gate_up"]["us"] * 1e-3
-        pk_tf = 2 * Mp * N * K / (pk * 1e-3) / 1e12
+        pxs = {k: v.cuda() for k, v in layer_inputs(synthetic, Mp, K, synthetic.prefill_case).items()}
+        pms, _ = layer_step_ms(b, torch, fp8, synthetic, weights, pxs, max(args.steps // 8, 20), 3)
+        lflops = sum(2 * Mp * n_ * k_ for n_, k_ in layer_shapes(synthetic).values())
+        six_pms = six_step_ms(b, torch, fp8, synthetic, weights, synthetic.prefill_case, Mp, max(args.steps // 8, 20), 3)
+        six_flops = sum(2 * Mp * n_ * k_ for n_, k_ in synthetic.SHAPES.values())
+        pk = per_kernel(b, torch, fp8, synthetic, rot, Mp, synthetic.prefill_case, 8, "mfma")
+        pk_us = pk["gate_up"]["us"]
+        pk_tf = 2 * Mp * N * Kg / (pk_us * 1e-6) / 1e12
+        psweep = {}
+        if not args.no_sweep:
+            for m in PREFILL_SWEEP_ROWS:
+                psweep[f"m{m}"] = per_kernel(b, torch, fp8, synthetic, rot, m, synthetic.prefill_case, 4, "mfma")
         result["prefill"] = {
-            "tokens": Mp, "ms_per_step": round(pms, 4), "TFLOP/s": round(flops / (pms * 1e-3) / 1e12, 1),
+            "tokens": Mp, "ms_per_step": round(pms, 4), "TFLOP/s": round(lflops / (pms * 1e-3) / 1e12, 1),
+            "step": "the decode step's layer (q/k/v merged, o, gate+up with SwiGLU epilogue, quantization of h, down) at M=2048",
+            "six_projections_step": {"ms": round(six_pms, 4), "TFLOP/s": round(six_flops / (six_pms * 1e-3) / 1e12, 1)},
             "roofline": {"bound": "mfma", "kernel": "gemm_prefill_pp_kernel (gate+up, N=24576 K=4096, M=2048)",
                          "achieved": round(pk_tf, 1), "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(pk_tf / FP8_PEAK_TFLOPS, 4), "avg_launch_us": round(pk * 1e3, 2),
+                         "frac": round(pk_tf / FP8_PEAK_TFLOPS, 4), "avg_launch_us": round(pk_us, 2),
                          "traffic": measured_traffic(f"prefill_gate_up_m{Mp}"),
-                         "flops_per_launch": 2 * Mp * N * K},
-            "kernels": pshape,
+                         "traffic_source": f"copied from {PMC_SUMMARY}, not measured in this run",
+                         "flops_per_launch": 2 * Mp * N * Kg},
+            "kernels": pk,
+            "kernels_sweep": psweep,
         }
-        log(f"bench: prefill step {pms:.3f} ms, kernels {pshape}")
+        log(f"bench: prefill layer step {pms:.3f} ms, six projections {six_pms:.3f} ms, kernels {pk}")
+    rot.drop()
+    del weights
+    torch.cuda.empty_cache()
 
     if not args.no_workloads:
         result["workloads"] = workloads(torch, b, fp8, synthetic, quantize_rows)

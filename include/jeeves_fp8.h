@@ -165,6 +165,34 @@ int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_
                            int64_t ldc, float* scales, void* h_out, int64_t ldh, const void* lora_a, int64_t lora_rank,
                            float* lora_t, void* stream);
 
+/* SwiGLU.forward's gate and up projections (model/model.py:581-584) as one
+ * fused FP8 linear with SwiGLU in the GEMM epilogue:
+ *   h[m,i] = bf16( bf16(silu(g[m,i])) * u[m,i] ),
+ * g and u being what jv_fp8_linear would output for the gate rows [0, I) and
+ * the up rows [I, 2I) of w (bias and LoRA included), so h is bitwise the
+ * result of running the two projections and then F.silu(gate) * up on bf16.
+ * w: [2I, K] e4m3fn, gate rows then up rows (row stride ldw, or ldw = 0: the
+ * tiled layout); w_scale, bias: [2I]; lora_b: [2I, rank]; h: [M, I] bf16 with
+ * row stride ldh >= I; h_amax: NULL or [M, I/16] uint16 receiving, per token
+ * and 16 channels of h, the largest |h| as a bf16 magnitude pattern (NaN
+ * sorts above inf). I a positive multiple of 16, K <= 16384. workspace:
+ * jv_fp8_linear_workspace_bytes(M, 2I, K, rank) bytes suffice; the fused
+ * GEMM never splits K. The gate+up output [M, 2I] never reaches memory. */
+int jv_fp8_linear_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
+                         const void* lora_a, const void* lora_b, int64_t lora_rank, float lora_scaling, void* h,
+                         int64_t ldh, uint16_t* h_amax, int64_t M, int64_t I, int64_t K, void* workspace,
+                         int64_t workspace_bytes, int32_t* tile_counters, int64_t n_counters, void* stream);
+
+/* The down projection's per-token quantization of h (quantize_rows
+ * semantics, as jv_fp8_quantize_rows_bf16), for jv_fp8_gemm: codes in the
+ * packed fragment order when ldc = 0, scales [M]; with lora_a [rank, I] bf16
+ * also lora_t [M, rank] = h A^T in fp32. h_amax: the maxima
+ * jv_fp8_linear_swiglu wrote for this h, or NULL. I a multiple of 16 (of 128
+ * when packed), at most 16384. */
+int jv_fp8_quantize_swiglu_output(const void* h, int64_t ldh, const uint16_t* h_amax, int64_t M, int64_t I, void* codes,
+                                  int64_t ldc, float* scales, const void* lora_a, int64_t lora_rank, float* lora_t,
+                                  void* stream);
+
 /* Tiled weight layout. Every GEMM entry point takes ldw = 0 to mean that w
  * holds the codes in the decode MFMA's fragment order instead of row-major:
  * for 16-row tile t = n/16 and 128-deep step s = k/128, a 2 KB fragment of

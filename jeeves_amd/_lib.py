@@ -34,6 +34,11 @@ SIGNATURES: dict[str, tuple] = {
                             c_void_p]),
     "jv_fp8_swiglu_quantize": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
                                        c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
+    "jv_fp8_linear_swiglu": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+                                     c_float, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64,
+                                     POINTER(c_int32), c_int64, c_void_p]),
+    "jv_fp8_quantize_swiglu_output": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p,
+                                              c_void_p, c_int64, c_void_p, c_void_p]),
     "jv_w8a16_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64]),
     "jv_w8a16_linear": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64,
                                 c_int64, c_void_p, c_int64, POINTER(c_int32), c_int64, c_void_p]),

@@ -70,17 +70,20 @@ int64_t partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
 bool packed_codes(int64_t K) { return jv::quant_chunks((int)K) != 0; }
 int64_t codes_bytes(int64_t M, int64_t K) { return packed_codes(K) ? jv::packed_x_bytes(M, K) : M * K; }
 
+// swiglu_half > 0: the fused SwiGLU epilogue (N = 2 swiglu_half weight rows,
+// gate then up; y is h [M, swiglu_half]; h_amax the optional maxima).
 int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, const uint8_t* w, int64_t ldw, const float* sw,
              const uint16_t* bias, const float* lora_t, const uint16_t* lora_b, int64_t rank, float lora_scaling, uint16_t* y,
              int64_t ldy, int64_t M, int64_t N, int64_t K, uint8_t* partial_ws, int64_t partial_ws_bytes,
-             int32_t* counters, int64_t n_counters, hipStream_t stream) {
+             int32_t* counters, int64_t n_counters, hipStream_t stream, int64_t swiglu_half = 0,
+             uint16_t* h_amax = nullptr) {
   const int cus = cu_count_of(-1);
   if (cus <= 0) return fail(JV_ERR_HIP, "cannot query the device's compute units");
   if ((uint64_t)M * (uint64_t)ldxq >= (1ull << 32) || (uint64_t)jv::packed_x_bytes(M, K) >= (1ull << 32))
     return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
-  jv::Epilogue ep{sx, sw, bias, lora_t, lora_b, lora_scaling, y, ldy};
+  jv::Epilogue ep{sx, sw, bias, lora_t, lora_b, lora_scaling, y, ldy, swiglu_half, h_amax};
   if (jv::decode_kernel_for(M, N, cus)) {
-    const jv::DecodePlan plan = jv::decode_plan(M, N, K, cus);
+    const jv::DecodePlan plan = jv::decode_plan(M, N, K, cus, swiglu_half != 0);
     const int splits = plan.splits;
     float* partial = nullptr;
     if (splits > 1) {
@@ -375,6 +378,56 @@ int jv_fp8_linear_noalloc(const void* x, int64_t ldx, const void* w, int64_t ldw
   return jv_fp8_linear(x, ldx, w, ldw, w_scale, bias, lora_a, lora_b, lora_rank, lora_scaling, y, ldy, M, N, K,
                        base + kNoAllocCounterBytes, kNoAllocWorkspaceBytes, reinterpret_cast<int32_t*>(base),
                        kNoAllocCounterSlots, stream);
+}
+
+int jv_fp8_linear_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
+                         const void* lora_a, const void* lora_b, int64_t lora_rank, float lora_scaling, void* h,
+                         int64_t ldh, uint16_t* h_amax, int64_t M, int64_t I, int64_t K, void* workspace,
+                         int64_t workspace_bytes, int32_t* tile_counters, int64_t n_counters, void* stream) {
+  if (I <= 0 || I % 16 || 2 * I > INT32_MAX)
+    return fail(JV_ERR_VALUE, "the fused SwiGLU needs an intermediate size divisible by 16, got %lld", (long long)I);
+  if (int rc = check_gemm_shape(M, 2 * I, K)) return rc;
+  if (int rc = check_lora(lora_rank, lora_a, lora_b)) return rc;
+  if (!packed_codes(K)) return fail(JV_ERR_VALUE, "the fused SwiGLU needs in_features <= 16384, got %lld", (long long)K);
+  if (M == 0) return JV_OK;
+  if (!aligned16(x) || (ldx * 2) % 16) return fail(JV_ERR_VALUE, "the fp8 GEMM needs 16-byte aligned operand rows");
+  if (ldh < I || !h || (h_amax && (reinterpret_cast<uintptr_t>(h_amax) & 1)))
+    return fail(JV_ERR_VALUE, "h needs a row stride of at least %lld", (long long)I);
+  if (int rc = check_weight(2 * I, K, ldw, w)) return rc;
+  const int64_t need = round_up(codes_bytes(M, K), 256) + round_up(M * 4, 256) + round_up(M * lora_rank * 4, 256);
+  if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255))
+    return fail(JV_ERR_VALUE, "workspace needs %lld bytes, 256-byte aligned", (long long)need);
+  uint8_t* ws = (uint8_t*)workspace;
+  uint8_t* codes = ws;
+  ws += round_up(codes_bytes(M, K), 256);
+  float* sx = (float*)ws;
+  ws += round_up(M * 4, 256);
+  float* lora_t = lora_rank ? (float*)ws : nullptr;
+  hipStream_t s = (hipStream_t)stream;
+  if (int rc = hip_status(jv::quant_rows_bf16((const uint16_t*)x, ldx, M, (int)K, codes, K, sx, (const uint16_t*)lora_a,
+                                              (int)lora_rank, lora_t, true, s),
+                          "activation quantization launch"))
+    return rc;
+  return run_gemm(codes, 0, true, sx, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t,
+                  (const uint16_t*)lora_b, lora_rank, lora_scaling, (uint16_t*)h, ldh, M, 2 * I, K, nullptr, 0,
+                  tile_counters, n_counters, s, I, h_amax);
+}
+
+int jv_fp8_quantize_swiglu_output(const void* h, int64_t ldh, const uint16_t* h_amax, int64_t M, int64_t I, void* codes,
+                                  int64_t ldc, float* scales, const void* lora_a, int64_t lora_rank, float* lora_t,
+                                  void* stream) {
+  if (M < 0 || I <= 0 || I % 16 || jv::quant_chunks((int)(I > INT32_MAX ? 0 : I)) == 0 || M > INT32_MAX)
+    return fail(JV_ERR_VALUE, "quantizing h needs 0 < I <= 16384 divisible by 16, got %lld", (long long)I);
+  if (int rc = check_lora(lora_rank, lora_a, lora_t)) return rc;
+  if (M == 0) return JV_OK;
+  const bool packed = ldc == 0;
+  if (packed && I % JV_FP8_BLOCK_K) return fail(JV_ERR_VALUE, "the packed layout needs I divisible by %d", JV_FP8_BLOCK_K);
+  if (!aligned16(h) || (ldh * 2) % 16 || !aligned16(codes) || ldc % 16)
+    return fail(JV_ERR_VALUE, "quantizing h needs 16-byte aligned rows");
+  (void)h_amax;
+  return hip_status(jv::quant_rows_bf16((const uint16_t*)h, ldh, M, (int)I, (uint8_t*)codes, ldc, scales,
+                                        (const uint16_t*)lora_a, (int)lora_rank, lora_t, packed, (hipStream_t)stream),
+                    "quantization of h launch");
 }
 
 }  // extern "C"

@@ -24,9 +24,28 @@ struct Epilogue {
   const float* lora_t;    // [M, RANK] fp32 or null
   const uint16_t* lora_b; // [N, RANK] bf16 or null
   float lora_scale;
-  uint16_t* y;            // [M, ldy] bf16
+  uint16_t* y;            // [M, ldy] bf16 (with SwiGLU: h [M, half])
   int64_t ldy;
+  // Fused SwiGLU (gate+up GEMMs): the weight's rows are gate [0, half) then up
+  // [half, 2 half); the kernels pair gate tile p with up tile p (logical
+  // channel order g0..g15 u0..u15 g16..., swiglu_channel) and store
+  // h = bf16(bf16(silu(y_gate)) * y_up) of width `half`, plus, when `parts` is
+  // set, the largest |h| (bf16 magnitude bits) of each token over each 16
+  // channels of h: parts[m * (half / 16) + c / 16].
+  int64_t half = 0;
+  uint16_t* parts = nullptr;
 };
+
+// Physical weight row of logical channel c in the SwiGLU pairing (c / 32 is
+// the pair p: 16 gate rows 16p.., then 16 up rows half + 16p..).
+__host__ __device__ __forceinline__ int64_t swiglu_channel(int64_t c, int64_t half) {
+  const int64_t p = c >> 5, r = c & 31;
+  return r < 16 ? p * 16 + r : half + p * 16 + (r - 16);
+}
+// The same for 16-row tiles: logical tile lt -> physical tile.
+__host__ __device__ __forceinline__ int64_t swiglu_tile(int64_t lt, int64_t half) {
+  return (lt & 1) ? (half >> 4) + (lt >> 1) : (lt >> 1);
+}
 
 // The value the caller rounds to bf16 once more: v itself, or bf16(v) + bias.
 // biasn: the bias of the channel, already loaded (used only when ep.bias is set).

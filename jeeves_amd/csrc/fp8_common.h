@@ -41,6 +41,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
 }
 
+// SwiGLU on bf16 values (SwiGLU.forward, model/model.py:583, as torch runs it
+// on bf16 tensors): silu(g) = g / (1 + exp(-g)) in fp32 rounded to bf16, times
+// up (exact in fp32), rounded to bf16.
+__device__ __forceinline__ uint32_t swiglu_bf16(uint32_t g16, uint32_t u16) {
+  const float g = bf16_to_f32(g16);
+  const float s = g / (1.0f + expf(-g));
+  const float sb = bf16_to_f32(f32_to_bf16(s));
+  return f32_to_bf16(sb * bf16_to_f32(u16));
+}
+
 // ---------------------------------------------------------------------------
 // e4m3fn encode, round to nearest even, NaN on overflow (|f| > 464), sign kept.
 // Written from the OCP FP8 v1.0 format definition; this is the semantics of

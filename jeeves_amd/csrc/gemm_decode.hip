@@ -31,11 +31,14 @@
 
 namespace jv {
 
-template <int MT, int RT, int WAVES, int UNROLL, bool PACKX, int RANK, bool PACKW>
+// SW: fused SwiGLU (gate+up weights, Epilogue::half): the wave's tiles come in
+// (gate p, up p) pairs, and the epilogue stores h (no split-K).
+template <int MT, int RT, int WAVES, int UNROLL, bool PACKX, int RANK, bool PACKW, bool SW = false>
 __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* __restrict__ xq, int64_t ldxq,
                                                                  const uint8_t* __restrict__ w, int64_t ldw, int M, int N,
                                                                  int K, int splits, float* __restrict__ partial,
                                                                  int* __restrict__ counters, Epilogue ep) {
+  static_assert(!SW || RT % 2 == 0, "SwiGLU pairs each gate tile with its up tile");
   __shared__ f32x4 red[WAVES][RT * MT][64];
   __shared__ int is_last;
   const int lane = threadIdx.x & 63;
@@ -61,12 +64,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   // Weights: row-major rows (lane -> row n0 + 16 rt + l%16, 32 bytes at k =
   // 32 (l/16)), or the tiled layout (lane -> 16 contiguous bytes of each
   // 1 KB half of the tile's 2 KB step fragment).
+  // With SwiGLU, logical tile group*RT + rt is gate tile p (rt even) or up
+  // tile p (rt odd) of pair p = group*RT/2 + rt/2.
   const uint8_t* wp[RT];
   const int ntiles = (N + 15) >> 4;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-    wp[rt] = PACKW ? w + (int64_t)min(group * RT + rt, ntiles - 1) * ksteps * 2048 + lane * 16
-                   : w + (int64_t)min(n0 + rt * 16 + li, N - 1) * ldw + lk;
+  for (int rt = 0; rt < RT; ++rt) {
+    const int lt = min(group * RT + rt, ntiles - 1);
+    const int64_t pt = SW ? swiglu_tile(lt, ep.half) : lt;
+    wp[rt] = PACKW ? w + pt * ksteps * 2048 + lane * 16
+                   : w + (SW ? pt * 16 + li : (int64_t)min(n0 + rt * 16 + li, N - 1)) * ldw + lk;
+  }
   const uint8_t* xp[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -76,18 +84,29 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   // and their scales and bias, loaded before the weight stream so the
   // epilogue does not wait for another memory round trip. Indices are clamped
   // so the loads are unconditional; a missing bias reads the scales instead.
-  constexpr int kOut = RT * MT * 256, kThreads = 64 * WAVES, kPer = (kOut + kThreads - 1) / kThreads;
-  float pre_sx[kPer], pre_sw[kPer], pre_b[kPer];
+  // With SwiGLU each output is one h channel hc = 16 p + nl, from gate row hc
+  // and up row half + hc (their scales and biases in the *2 arrays).
+  constexpr int kOut = (SW ? RT / 2 : RT) * MT * 256, kThreads = 64 * WAVES, kPer = (kOut + kThreads - 1) / kThreads;
+  float pre_sx[kPer], pre_sw[kPer], pre_b[kPer], pre_sw2[SW ? kPer : 1], pre_b2[SW ? kPer : 1];
   {
     const uint16_t* bsrc = ep.bias ? ep.bias : reinterpret_cast<const uint16_t*>(ep.sw);
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int idx = min((int)threadIdx.x + j * kThreads, kOut - 1);
       const int t = idx >> 8, e = idx & 255;
-      const int m = min((t % MT) * 16 + (e >> 4), M - 1), n = min(n0 + (t / MT) * 16 + (e & 15), N - 1);
+      const int m = min((t % MT) * 16 + (e >> 4), M - 1);
       pre_sx[j] = ep.sx[m];
-      pre_sw[j] = ep.sw[n];
-      pre_b[j] = bf16_to_f32(bsrc[n]);
+      if constexpr (SW) {
+        const int64_t hc = (int64_t)(group * (RT / 2) + t / MT) * 16 + (e & 15);
+        pre_sw[j] = ep.sw[hc];
+        pre_b[j] = bf16_to_f32(bsrc[hc]);
+        pre_sw2[j] = ep.sw[ep.half + hc];
+        pre_b2[j] = bf16_to_f32(bsrc[ep.half + hc]);
+      } else {
+        const int n = min(n0 + (t / MT) * 16 + (e & 15), N - 1);
+        pre_sw[j] = ep.sw[n];
+        pre_b[j] = bf16_to_f32(bsrc[n]);
+      }
     }
   }
 
@@ -149,6 +168,45 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   // with rows = weight channels and cols = tokens). Threads walk n fastest so
   // consecutive threads store consecutive channels of one token.
   const float* redf = reinterpret_cast<const float*>(&red[0][0][0]);
+  if constexpr (SW) {
+    // h[m, hc] = bf16(bf16(silu(y_gate)) * y_up), y = the bf16 outputs the
+    // unfused GEMM would store; thread groups of 16 (one token, 16 channels)
+    // also take the largest |h| for the row's quantizer. Every break and
+    // shuffle below is uniform across a wave (kOut and kThreads are multiples
+    // of 64).
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int idx = (int)threadIdx.x + j * kThreads;
+      if (kOut % kThreads != 0 && idx >= kOut) break;
+      const int t = idx >> 8, q = t / MT, mt = t % MT, e = idx & 255, ml = e >> 4, nl = e & 15;
+      const int off = ml + 16 * (nl >> 2);
+      const int src_g = (((2 * q) * MT + mt) * 64 + off) * 4 + (nl & 3);
+      const int src_u = (((2 * q + 1) * MT + mt) * 64 + off) * 4 + (nl & 3);
+      float sum_g = 0.0f, sum_u = 0.0f;
+#pragma unroll
+      for (int wv = 0; wv < WAVES; ++wv) {
+        sum_g += redf[wv * RT * MT * 256 + src_g];
+        sum_u += redf[wv * RT * MT * 256 + src_u];
+      }
+      const int m = mt * 16 + ml;
+      const int64_t hc = (int64_t)(group * (RT / 2) + q) * 16 + nl;
+      uint32_t hv = 0;
+      if (m < M) {
+        const uint32_t yg = f32_to_bf16(epilogue_value<RANK>(ep, sum_g, m, (int)hc, pre_sx[j], pre_sw[j], pre_b[j]));
+        const uint32_t yu =
+            f32_to_bf16(epilogue_value<RANK>(ep, sum_u, m, (int)(ep.half + hc), pre_sx[j], pre_sw2[j], pre_b2[j]));
+        hv = swiglu_bf16(yg, yu);
+        ep.y[(int64_t)m * ep.ldy + hc] = (uint16_t)hv;
+      }
+      if (ep.parts) {
+        uint32_t mx = hv & 0x7FFFu;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+        if (nl == 0 && m < M) ep.parts[(int64_t)m * (ep.half >> 4) + (hc >> 4)] = (uint16_t)mx;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int idx = (int)threadIdx.x + j * kThreads;
@@ -203,11 +261,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
 // the burst's operands fit the registers without spilling.
 constexpr int decode_unroll(int mt, int rt, int w) { return rt + mt > 4 ? 2 : ((w == 8 || rt + mt > 3) ? 4 : 8); }
 
-DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count) {
+DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count, bool swiglu) {
   DecodePlan p;
   const int64_t tiles = (N + 15) / 16;
   const int64_t mt = (M + 15) / 16;
-  p.rt = tiles >= 4 * (int64_t)cu_count ? 2 : 1;
+  // A fused SwiGLU wave owns one gate tile and its up tile.
+  p.rt = swiglu || tiles >= 4 * (int64_t)cu_count ? 2 : 1;
   // Four waves take 8 k steps each in one burst up to K = 4096; longer rows
   // use eight waves in bursts of 4. More token tiles shorten the burst to
   // bound the registers it holds.
@@ -218,7 +277,7 @@ DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count) {
   // Splitting K across workgroups only pays when the tiles cannot occupy an
   // eighth of the CUs: below that the launch is latency-bound either way.
   p.splits = 1;
-  if (groups * 8 < cu_count) {
+  if (!swiglu && groups * 8 < cu_count) {
     int64_t s = (cu_count + groups - 1) / groups;
     const int64_t max_s = (K / 128) / p.waves;
     if (s > max_s) s = max_s;
@@ -228,46 +287,50 @@ DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count) {
   return p;
 }
 
-template <int MT, int RT, int W, int U, bool PACKX, int RANK>
+template <int MT, int RT, int W, int U, bool PACKX, int RANK, bool SW>
 static void launch_decode(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
                           const DecodePlan& p, float* partial, int* counters, const Epilogue& ep, hipStream_t stream) {
   const dim3 grid((unsigned)p.groups, (unsigned)p.splits), block(64 * W);
   if (ldw == 0)
-    gemm_decode_kernel<MT, RT, W, U, PACKX, RANK, true>
+    gemm_decode_kernel<MT, RT, W, U, PACKX, RANK, true, SW>
         <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, p.splits, partial, counters, ep);
   else
-    gemm_decode_kernel<MT, RT, W, U, PACKX, RANK, false>
+    gemm_decode_kernel<MT, RT, W, U, PACKX, RANK, false, SW>
         <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, p.splits, partial, counters, ep);
 }
 
-template <int MT, int RT, bool PACKX, int RANK>
+template <int MT, int RT, bool PACKX, int RANK, bool SW>
 static void launch_decode_wu(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
                              const DecodePlan& p, float* partial, int* counters, const Epilogue& ep, hipStream_t stream) {
   constexpr int U4 = decode_unroll(MT, RT, 4), U8 = decode_unroll(MT, RT, 8);
   if (p.waves == 8)
-    launch_decode<MT, RT, 8, U8, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+    launch_decode<MT, RT, 8, U8, PACKX, RANK, SW>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
   else
-    launch_decode<MT, RT, 4, U4, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+    launch_decode<MT, RT, 4, U4, PACKX, RANK, SW>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
 }
 
-template <int MT, bool PACKX, int RANK>
+template <int MT, bool PACKX, int RANK, bool SW>
 static void launch_decode_rt(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
                              const DecodePlan& p, float* partial, int* counters, const Epilogue& ep, hipStream_t stream) {
-  if (p.rt == 2)
-    launch_decode_wu<MT, 2, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
-  else
-    launch_decode_wu<MT, 1, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+  if constexpr (SW) {
+    launch_decode_wu<MT, 2, PACKX, RANK, true>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+  } else {
+    if (p.rt == 2)
+      launch_decode_wu<MT, 2, PACKX, RANK, false>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+    else
+      launch_decode_wu<MT, 1, PACKX, RANK, false>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+  }
 }
 
-template <bool PACKX, int RANK>
+template <bool PACKX, int RANK, bool SW = false>
 static hipError_t launch_decode_mt(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
                                    const DecodePlan& p, float* partial, int* counters, const Epilogue& ep,
                                    hipStream_t stream) {
   switch ((M + 15) / 16) {
-    case 1: launch_decode_rt<1, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
-    case 2: launch_decode_rt<2, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
-    case 3: launch_decode_rt<3, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
-    case 4: launch_decode_rt<4, PACKX, RANK>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
+    case 1: launch_decode_rt<1, PACKX, RANK, SW>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
+    case 2: launch_decode_rt<2, PACKX, RANK, SW>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
+    case 3: launch_decode_rt<3, PACKX, RANK, SW>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
+    case 4: launch_decode_rt<4, PACKX, RANK, SW>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -277,6 +340,12 @@ hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, bool packed_x, const uin
                        const DecodePlan& plan, float* partial, int* counters, const Epilogue& ep, int rank,
                        hipStream_t stream) {
   if (M < 1 || M > kDecodeMaxRows || (rank != 0 && rank != 16)) return hipErrorInvalidValue;
+  if (ep.half) {
+    // Fused SwiGLU: packed activation codes only (jv_fp8_linear_swiglu packs them), one gate/up pair per wave.
+    if (!packed_x || plan.rt != 2 || plan.splits != 1 || 2 * ep.half != N || ep.half % 16) return hipErrorInvalidValue;
+    return rank == 16 ? launch_decode_mt<true, 16, true>(xq, ldxq, w, ldw, M, N, K, plan, partial, counters, ep, stream)
+                      : launch_decode_mt<true, 0, true>(xq, ldxq, w, ldw, M, N, K, plan, partial, counters, ep, stream);
+  }
   if (packed_x)
     return rank == 16 ? launch_decode_mt<true, 16>(xq, ldxq, w, ldw, M, N, K, plan, partial, counters, ep, stream)
                       : launch_decode_mt<true, 0>(xq, ldxq, w, ldw, M, N, K, plan, partial, counters, ep, stream);

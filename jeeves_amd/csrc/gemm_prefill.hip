@@ -103,8 +103,9 @@ __device__ __forceinline__ void load_lora(LoraOperands<TN, TM>& o, const Epilogu
   const int h = lane >> 5;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int n = min(nb + j * 32 + (lane & 31), N - 1);
-    o.b[j] = *reinterpret_cast<const i32x4*>(ep.lora_b + (int64_t)n * 16 + 8 * h);
+    const int c = min(nb + j * 32 + (lane & 31), N - 1);
+    const int64_t n = ep.half ? swiglu_channel(c, ep.half) : c;
+    o.b[j] = *reinterpret_cast<const i32x4*>(ep.lora_b + n * 16 + 8 * h);
   }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -211,7 +212,102 @@ __device__ __forceinline__ void store_tile(uint8_t* lds, const float* scale_lds,
   }
 }
 
-template <int BM, int BN, int WGM, int WGN, int BK, int STAGES, int RANK, bool PACKW, bool PACKX>
+// Epilogue of both FP8 prefill kernels with the fused SwiGLU (Epilogue::half):
+// the tile's logical channels come in 32-channel blocks of 16 gate and the 16
+// matching up channels, so in each 32x32 accumulator block a lane's registers
+// 0-7 are gate channels and 8-15 the up channels of the same h channels (the
+// register quad q + 2 pairs with q). h = bf16(bf16(silu(y_gate)) * y_up) with
+// y = the bf16 output the unfused GEMM would store (bias in bf16 after it).
+// The h tile (BM tokens x BN/2 channels) goes through LDS as in store_tile;
+// with ep.parts set, each token's largest |h| over each 16 h channels goes to
+// parts[m * (half / 16) + h_channel / 16].
+template <int BM, int BN, int WGM, int WGN, int RANK>
+__device__ __forceinline__ void store_tile_sw(uint8_t* lds, const float* scale_lds,
+                                              const f32x16 (&acc)[BN / WGN / 32][BM / WGM / 32], const Epilogue& ep,
+                                              int m0, int n0, int M, int N, int wm, int wn, int lane) {
+  constexpr int NW = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int HBN = BN / 2;               // h channels per tile
+  constexpr int OUT_CH = HBN * 2 / 16;      // 16-byte chunks per h tile row
+  static_assert(OUT_CH <= 32 && (OUT_CH & (OUT_CH - 1)) == 0, "output tile width");
+  static_assert(RANK == 0 || RANK == 16, "LoRA rank");
+  LoraOperands<TN, TM> lo;
+  if constexpr (RANK > 0) load_lora(lo, ep, n0 + wn * WN, m0 + wm * WM, M, N, lane);
+  float sxm[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) sxm[i] = scale_lds[wm * WM + i * 32 + (lane & 31)];
+  lds_barrier();
+  const int64_t hparts = ep.half >> 4;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int cb = wn * WN + j * 32;  // the block's first logical channel in the tile
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int ml = wm * WM + i * 32 + (lane & 31);
+      f32x16 lora;
+      if constexpr (RANK > 0) lora = lora_block(lo.b[j], lo.t[i]);
+      uint32_t mx = 0;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int o = 8 * q + 4 * (lane >> 5);  // gate channel offset in the block; its up channel is o + 16
+        const float4 sg = *reinterpret_cast<const float4*>(scale_lds + BM + cb + o);
+        const float4 su = *reinterpret_cast<const float4*>(scale_lds + BM + cb + 16 + o);
+        const float swg[4] = {sg.x, sg.y, sg.z, sg.w}, swu[4] = {su.x, su.y, su.z, su.w};
+        uint32_t hv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float vg = (acc[j][i][4 * q + e] * sxm[i]) * swg[e];
+          float vu = (acc[j][i][4 * (q + 2) + e] * sxm[i]) * swu[e];
+          if constexpr (RANK > 0) {
+            vg += lora[4 * q + e] * ep.lora_scale;
+            vu += lora[4 * (q + 2) + e] * ep.lora_scale;
+          }
+          if (ep.bias) {
+            const int c = min(n0 + cb + o + e, N - 1);
+            vg = with_bias(ep, vg, bf16_to_f32(ep.bias[swiglu_channel(c, ep.half)]));
+            vu = with_bias(ep, vu, bf16_to_f32(ep.bias[swiglu_channel(c + 16, ep.half)]));
+          }
+          hv[e] = swiglu_bf16(f32_to_bf16(vg), f32_to_bf16(vu));
+          mx = max(mx, hv[e] & 0x7FFFu);
+        }
+        const int hl = cb / 2 + o;  // h channel within the tile
+        const int chunk = (hl >> 3) ^ (ml % OUT_CH);
+        *reinterpret_cast<uint2*>(lds + ml * (HBN * 2) + chunk * 16 + (hl & 4) * 2) =
+            uint2{hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16)};
+      }
+      if (ep.parts) {
+        // blocks past the last h channel (a ragged last tile) have no slot
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
+        if (lane < 32 && m0 + ml < M && (n0 + cb) / 2 < ep.half)
+          ep.parts[(int64_t)(m0 + ml) * hparts + (n0 + cb) / 32] = (uint16_t)mx;
+      }
+    }
+  }
+  lds_barrier();
+  const int64_t h0 = n0 / 2;
+  const bool y_vec = ((ep.ldy | ep.half) & 7) == 0 && (reinterpret_cast<uintptr_t>(ep.y) & 15) == 0;
+  constexpr int NT = 64 * NW;
+#pragma unroll 4
+  for (int c = threadIdx.x; c < BM * OUT_CH; c += NT) {
+    const int ml = c / OUT_CH, ch = c % OUT_CH;
+    const int m = m0 + ml;
+    const int64_t hn = h0 + ch * 8;
+    if (m >= M || hn >= ep.half) continue;
+    const uint4 v = *reinterpret_cast<const uint4*>(lds + ml * (HBN * 2) + (ch ^ (ml % OUT_CH)) * 16);
+    uint16_t* dst = ep.y + (int64_t)m * ep.ldy + hn;
+    if (y_vec) {
+      *reinterpret_cast<uint4*>(dst) = v;
+    } else {
+      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (hn + e < ep.half) dst[e] = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+}
+
+template <int BM, int BN, int WGM, int WGN, int BK, int STAGES, int RANK, bool PACKW, bool PACKX, bool SW = false>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint8_t* __restrict__ xq, int64_t ldx,
                                                                       const uint8_t* __restrict__ w, int64_t ldw, int M,
                                                                       int N, int K, int tiles_m, int tiles_n, int group_m,
@@ -275,10 +371,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
       const int tt = BK == 128 ? gw >> 1 : gw;
       const int h = BK == 128 ? gw & 1 : lane >> 5;
       const int lp = BK == 128 ? lane : lane & 31;
-      const int tile = min((n0 >> 4) + tt, ntiles - 1);
-      src[i] = w + (((int64_t)tile * (K >> 7)) * 2 + h) * 1024 + lp * 16;
+      const int lt = min((n0 >> 4) + tt, ntiles - 1);
+      const int64_t tile = SW ? swiglu_tile(lt, ep.half) : lt;
+      src[i] = w + ((tile * (K >> 7)) * 2 + h) * 1024 + lp * 16;
     } else {
-      src[i] = w + (int64_t)min(n0 + r - BM, N - 1) * ldw + chunk * 16;
+      const int c = min(n0 + r - BM, N - 1);
+      src[i] = w + (SW ? swiglu_channel(c, ep.half) : (int64_t)c) * ldw + chunk * 16;
     }
   }
 
@@ -314,7 +412,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
   // covers them), out of the epilogue's critical path.
   for (int t = wave * 64; t < BM + BN; t += NW * 64) {
     const int r = t + lane;
-    const float* sp = r < BM ? ep.sx + min(m0 + r, M - 1) : ep.sw + min(n0 + r - BM, N - 1);
+    const int c = min(n0 + r - BM, N - 1);
+    const float* sp = r < BM ? ep.sx + min(m0 + r, M - 1) : ep.sw + (SW ? swiglu_channel(c, ep.half) : (int64_t)c);
     typedef __attribute__((address_space(3))) void lds_void;
     typedef __attribute__((address_space(1))) void global_void;
     __builtin_amdgcn_global_load_lds((global_void*)sp, (lds_void*)(scale_lds + t), 4, 0, 0);
@@ -422,7 +521,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
     }
   }
 
-  store_tile<BM, BN, WGM, WGN, RANK>(lds, scale_lds, acc, ep, m0, n0, M, N, wm, wn, lane);
+  if constexpr (SW) store_tile_sw<BM, BN, WGM, WGN, RANK>(lds, scale_lds, acc, ep, m0, n0, M, N, wm, wn, lane);
+  else store_tile<BM, BN, WGM, WGN, RANK>(lds, scale_lds, acc, ep, m0, n0, M, N, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -446,7 +546,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
 // before phase 2j-1, so each wave waits for its own copies of stage j+1 before
 // the barrier that ends phase 2j.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int STAGES, int RANK, bool PACKW, bool PACKX>
+template <int BM, int BN, int STAGES, int RANK, bool PACKW, bool PACKX, bool SW = false>
 __global__ __launch_bounds__(512) void gemm_prefill_pp_kernel(const uint8_t* __restrict__ xq, int64_t ldx,
                                                               const uint8_t* __restrict__ w, int64_t ldw, int M, int N,
                                                               int K, int tiles_m, int tiles_n, int group_m, Epilogue ep) {
@@ -484,10 +584,12 @@ __global__ __launch_bounds__(512) void gemm_prefill_pp_kernel(const uint8_t* __r
     } else if (r < BM) {
       src[i] = xq + (int64_t)min(m0 + r, M - 1) * ldx + chunk * 16;
     } else if (PACKW) {
-      const int tile = min((n0 >> 4) + (g - BM / RPL), ntiles - 1);
-      src[i] = w + (((int64_t)tile * (K >> 7)) * 2 + (lane >> 5)) * 1024 + (lane & 31) * 16;
+      const int lt = min((n0 >> 4) + (g - BM / RPL), ntiles - 1);
+      const int64_t tile = SW ? swiglu_tile(lt, ep.half) : lt;
+      src[i] = w + ((tile * (K >> 7)) * 2 + (lane >> 5)) * 1024 + (lane & 31) * 16;
     } else {
-      src[i] = w + (int64_t)min(n0 + r - BM, N - 1) * ldw + chunk * 16;
+      const int c = min(n0 + r - BM, N - 1);
+      src[i] = w + (SW ? swiglu_channel(c, ep.half) : (int64_t)c) * ldw + chunk * 16;
     }
   }
   auto issue_stage = [&](int kt) {
@@ -516,7 +618,8 @@ __global__ __launch_bounds__(512) void gemm_prefill_pp_kernel(const uint8_t* __r
 
   for (int t = wave * 64; t < BM + BN; t += NW * 64) {
     const int r = t + lane;
-    const float* sp = r < BM ? ep.sx + min(m0 + r, M - 1) : ep.sw + min(n0 + r - BM, N - 1);
+    const int c = min(n0 + r - BM, N - 1);
+    const float* sp = r < BM ? ep.sx + min(m0 + r, M - 1) : ep.sw + (SW ? swiglu_channel(c, ep.half) : (int64_t)c);
     typedef __attribute__((address_space(3))) void lds_void;
     typedef __attribute__((address_space(1))) void global_void;
     __builtin_amdgcn_global_load_lds((global_void*)sp, (lds_void*)(scale_lds + t), 4, 0, 0);
@@ -600,7 +703,8 @@ __global__ __launch_bounds__(512) void gemm_prefill_pp_kernel(const uint8_t* __r
       barrier_only();
     }
   }
-  store_tile<BM, BN, WGM, WGN, RANK>(lds, scale_lds, acc, ep, m0, n0, M, N, wm, wn, lane);
+  if constexpr (SW) store_tile_sw<BM, BN, WGM, WGN, RANK>(lds, scale_lds, acc, ep, m0, n0, M, N, wm, wn, lane);
+  else store_tile<BM, BN, WGM, WGN, RANK>(lds, scale_lds, acc, ep, m0, n0, M, N, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -809,7 +913,20 @@ static hipError_t launch_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* 
 #define JV_PREFILL_LAUNCH_X(R, PW)             \
   if (ldx == 0) JV_PREFILL_LAUNCH(R, PW, true); \
   else JV_PREFILL_LAUNCH(R, PW, false);
-  if (rank == 16) {
+  if (ep.half) {
+    // fused SwiGLU: packed activation codes only
+#define JV_PREFILL_LAUNCH_SW(R, PW)                                      \
+  gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, R, PW, true, true>   \
+      <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep)
+    if (rank == 16) {
+      if (ldw == 0) JV_PREFILL_LAUNCH_SW(16, true);
+      else JV_PREFILL_LAUNCH_SW(16, false);
+    } else {
+      if (ldw == 0) JV_PREFILL_LAUNCH_SW(0, true);
+      else JV_PREFILL_LAUNCH_SW(0, false);
+    }
+#undef JV_PREFILL_LAUNCH_SW
+  } else if (rank == 16) {
     if (ldw == 0) { JV_PREFILL_LAUNCH_X(16, true) }
     else { JV_PREFILL_LAUNCH_X(16, false) }
   } else {
@@ -837,11 +954,22 @@ static hipError_t launch_prefill_pp(const uint8_t* xq, int64_t ldx, const uint8_
     if (ldx == 0) JV_PREFILL_PP_LAUNCH(R, false, true);    \
     else JV_PREFILL_PP_LAUNCH(R, false, false);            \
   }
-  if (rank == 16) {
+#define JV_PREFILL_PP_LAUNCH_SW(R, PW) \
+  gemm_prefill_pp_kernel<BM, BN, STAGES, R, PW, true, true><<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep)
+  if (ep.half) {
+    if (rank == 16) {
+      if (ldw == 0) JV_PREFILL_PP_LAUNCH_SW(16, true);
+      else JV_PREFILL_PP_LAUNCH_SW(16, false);
+    } else {
+      if (ldw == 0) JV_PREFILL_PP_LAUNCH_SW(0, true);
+      else JV_PREFILL_PP_LAUNCH_SW(0, false);
+    }
+  } else if (rank == 16) {
     JV_PREFILL_PP_LAUNCH_R(16)
   } else {
     JV_PREFILL_PP_LAUNCH_R(0)
   }
+#undef JV_PREFILL_PP_LAUNCH_SW
 #undef JV_PREFILL_PP_LAUNCH_R
 #undef JV_PREFILL_PP_LAUNCH
   return hipGetLastError();
@@ -876,17 +1004,13 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
                         const Epilogue& ep, int rank, PrefillTile t, hipStream_t stream) {
   if (rank != 0 && rank != 16) return hipErrorInvalidValue;
   if (K % t.bk || K % 128) return hipErrorInvalidValue;
+  if (ep.half && (ldx != 0 || 2 * ep.half != N || ep.half % 16)) return hipErrorInvalidValue;
   if (t.pingpong) {
     if (t.wgm != 2 || t.wgn != 4 || t.bk != 64) return hipErrorInvalidValue;
 #define JV_PREFILL_PP_CASE(BM_, BN_, ST_) \
   if (t.bm == BM_ && t.bn == BN_ && t.stages == ST_) \
     return launch_prefill_pp<BM_, BN_, ST_>(xq, ldx, w, ldw, M, N, K, ep, rank, t.group_m, stream);
     JV_PREFILL_PP_CASE(256, 256, 4)
-#ifdef JV_PREFILL_ALL_TILES
-    JV_PREFILL_PP_CASE(256, 256, 3)
-    JV_PREFILL_PP_CASE(256, 128, 4)
-    JV_PREFILL_PP_CASE(256, 128, 3)
-#endif
 #undef JV_PREFILL_PP_CASE
     return hipErrorInvalidValue;
   }
@@ -897,24 +1021,6 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
   JV_PREFILL_CASE(256, 128, 2, 4, 128, 3)
   JV_PREFILL_CASE(128, 128, 2, 2, 128, 4)
   JV_PREFILL_CASE(64, 64, 2, 2, 128, 4)
-#ifdef JV_PREFILL_ALL_TILES
-  // Further shapes for launch-shape sweeps.
-  JV_PREFILL_CASE(256, 256, 2, 4, 64, 4)
-  JV_PREFILL_CASE(256, 256, 4, 2, 64, 4)
-  JV_PREFILL_CASE(256, 256, 2, 4, 64, 3)
-  JV_PREFILL_CASE(256, 128, 2, 4, 64, 4)
-  JV_PREFILL_CASE(128, 256, 2, 4, 128, 3)
-  JV_PREFILL_CASE(128, 128, 2, 2, 64, 4)
-  JV_PREFILL_CASE(128, 64, 2, 2, 128, 4)
-  JV_PREFILL_CASE(64, 128, 2, 2, 128, 4)
-  JV_PREFILL_CASE(128, 64, 4, 1, 128, 4)
-  JV_PREFILL_CASE(64, 64, 2, 2, 128, 3)
-  JV_PREFILL_CASE(128, 64, 2, 2, 128, 3)
-  JV_PREFILL_CASE(128, 128, 2, 2, 64, 3)
-  JV_PREFILL_CASE(256, 128, 2, 4, 64, 3)
-  JV_PREFILL_CASE(64, 128, 2, 2, 128, 3)
-  JV_PREFILL_CASE(64, 64, 2, 2, 64, 4)
-#endif
 #undef JV_PREFILL_CASE
   return hipErrorInvalidValue;
 }

@@ -89,13 +89,16 @@ hipError_t quant_swiglu_bf16(const uint16_t* gate, int64_t ldg, const uint16_t* 
 hipError_t quant_rows_f32(const float* x, int64_t ldx, int64_t M, int K, uint8_t* codes, int64_t ldc, float* scales,
                           hipStream_t stream);
 
-DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count);
+// swiglu: the plan of a fused SwiGLU gate+up GEMM (a gate/up tile pair per
+// wave, no split-K).
+DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count, bool swiglu = false);
 hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, bool packed_x, const uint8_t* w, int64_t ldw, int M, int N, int K,
                        const DecodePlan& plan, float* partial, int* counters, const Epilogue& ep, int rank,
                        hipStream_t stream);
 
 PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count);
 // ldx = 0: packed activation codes (packed_x_offset); ldw = 0: tiled weights.
+// ep.half != 0: fused SwiGLU epilogue (packed codes only, N = 2 half).
 hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
                         const Epilogue& ep, int rank, PrefillTile tile, hipStream_t stream);
 

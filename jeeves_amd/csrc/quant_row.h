@@ -25,14 +25,6 @@
 
 namespace jv {
 
-// silu in fp32 rounded to bf16, times up, rounded to bf16.
-__device__ __forceinline__ uint32_t swiglu_bf16(uint32_t g16, uint32_t u16) {
-  const float g = bf16_to_f32(g16);
-  const float s = g / (1.0f + expf(-g));
-  const float sb = bf16_to_f32(f32_to_bf16(s));
-  return f32_to_bf16(sb * bf16_to_f32(u16));
-}
-
 __device__ __forceinline__ uint32_t swiglu_pair(uint32_t g2, uint32_t u2) {
   return swiglu_bf16(g2 & 0xFFFFu, u2 & 0xFFFFu) | (swiglu_bf16(g2 >> 16, u2 >> 16) << 16);
 }

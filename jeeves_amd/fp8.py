@@ -374,6 +374,85 @@ def swiglu_quantize(gate: torch.Tensor, up: torch.Tensor, *, lora_a: torch.Tenso
     return out
 
 
+def gate_up_swiglu(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *, bias: torch.Tensor | None = None,
+                   lora: tuple[torch.Tensor, torch.Tensor, float] | None = None, tiled: bool = False,
+                   amax: bool = False) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
+    """``F.silu(gate(x)) * up(x)`` (``model/model.py:583``) with both
+    projections as one FP8 GEMM whose epilogue applies SwiGLU (C ABI
+    ``jv_fp8_linear_swiglu``): ``weight`` [2I, K] holds the gate rows, then the
+    up rows (the fused gate+up linear), ``scale``/``bias`` [2I], LoRA B
+    [2I, r]. Returns h bf16 [M, I], bitwise ``swiglu(fp8_matmul(x, ...))`` of
+    the two halves; with ``amax`` also the per-token largest |h| over each
+    16 channels (uint16 bf16 magnitude patterns [M, I/16])."""
+    M, K = x.shape
+    N = weight.shape[0]
+    _check_weight(K, weight)
+    if N % 32:
+        raise ValueError(f"the fused gate+up weight needs 2I rows with I divisible by 16, got {N}")
+    I = N // 2
+    a, b, rank, scaling = _check_lora(lora, K, N)
+    dev = x.device
+    _check_operands(dev, N, weight, scale, bias, a, b)
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    if not _rows_aligned(x, 2):
+        x = x.contiguous()
+    w, ldw = _weight_operand(weight, tiled)
+    h = torch.empty(M, I, device=dev, dtype=torch.bfloat16)
+    parts = torch.empty(M, I // 16, device=dev, dtype=torch.int16) if amax else None
+    if M:
+        bias = bias.to(torch.bfloat16).contiguous() if bias is not None else None
+        scale = scale.to(torch.float32).contiguous()
+        L = _lib.lib()
+        with torch.cuda.device(dev):
+            ws_bytes = L.jv_fp8_linear_workspace_bytes(M, N, K, rank)
+            if ws_bytes < 0:
+                _lib.check(_lib.JV_ERR_HIP)
+            ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+            _lib.check(L.jv_fp8_linear_swiglu(x.data_ptr(), x.stride(0), w.data_ptr(), ldw, scale.data_ptr(),
+                                              bias.data_ptr() if bias is not None else None, a.data_ptr() if rank else None,
+                                              b.data_ptr() if rank else None, rank, scaling, h.data_ptr(), I,
+                                              parts.data_ptr() if parts is not None else None, M, I, K, ws.data_ptr(),
+                                              ws_bytes, None, 0, _stream(dev)))
+    return (h, parts) if amax else h
+
+
+def quantize_swiglu_output(h: torch.Tensor, amax: torch.Tensor | None = None, *, lora_a: torch.Tensor | None = None,
+                           packed: bool = True) -> tuple[torch.Tensor, ...]:
+    """The down projection's per-token quantization of h (``quantize_rows``
+    semantics; C ABI ``jv_fp8_quantize_swiglu_output``). Returns
+    ``(codes, scales)``, plus ``t = h A^T`` (float32 [M,r]) with ``lora_a``.
+    ``packed``: codes as a flat uint8 buffer in the GEMMs' fragment order (for
+    ``fp8_matmul_quantized(..., packed_rows=M)``); ``amax``: the maxima
+    ``gate_up_swiglu(..., amax=True)`` returned with h."""
+    M, I = h.shape
+    dev = h.device
+    if dev.type != "cuda" or h.dtype != torch.bfloat16:
+        raise ValueError(f"h must be bf16 on a HIP device, got {h.dtype} on {dev}")
+    if not _rows_aligned(h, 2):
+        h = h.contiguous()
+    codes = torch.empty(packed_codes_bytes(M, I) if packed else (M, I), dtype=torch.uint8, device=dev)
+    scales = torch.empty(M, dtype=torch.float32, device=dev)
+    rank, t = 0, None
+    if lora_a is not None:
+        rank = lora_a.shape[0]
+        if rank not in LORA_RANKS or lora_a.shape[1] != I:
+            raise ValueError(f"lora_a must be [r,{I}] with r in {LORA_RANKS}, got {tuple(lora_a.shape)}")
+        lora_a = lora_a.to(torch.bfloat16).contiguous()
+        t = torch.empty(M, rank, dtype=torch.float32, device=dev)
+    if amax is not None and (amax.shape != (M, I // 16) or amax.element_size() != 2 or not amax.is_contiguous()):
+        raise ValueError(f"amax must be a contiguous 16-bit [{M}, {I // 16}] tensor")
+    if M:
+        with torch.cuda.device(dev):
+            _lib.check(_lib.lib().jv_fp8_quantize_swiglu_output(h.data_ptr(), h.stride(0),
+                                                                amax.data_ptr() if amax is not None else None, M, I,
+                                                                codes.data_ptr(), 0 if packed else I, scales.data_ptr(),
+                                                                lora_a.data_ptr() if rank else None, rank,
+                                                                t.data_ptr() if rank else None, _stream(dev)))
+    out: tuple[torch.Tensor, ...] = (codes if packed else codes.view(FP8), scales)
+    return out + (t,) if rank else out
+
+
 class FP8Linear(nn.Module):
     """``inference/fp8.py:151-185``: buffers ``weight`` (float8_e4m3fn [N,K],
     row-major, as the reference keeps it) and ``scale`` (float32 [N]),
@@ -500,9 +579,11 @@ class FP8Linear(nn.Module):
 
 
 class FP8SwiGLU(nn.Module):
-    """``SwiGLU`` (``model/model.py:574-584``) over FP8 projections: one fused
-    gate+up GEMM (gate rows first, then up rows), the silu-product fused with
-    the down projection's activation quantization, then the down GEMM."""
+    """``SwiGLU`` (``model/model.py:574-584``) over FP8 projections: the gate
+    and up projections as one FP8 GEMM (``gate_up``: gate rows first, then up
+    rows) whose epilogue applies SwiGLU and writes h, the down projection's
+    quantization of h, then the down GEMM. The gate+up output never reaches
+    memory; the result is bitwise that of the separate steps."""
 
     def __init__(self, gate_up: FP8Linear, down: FP8Linear):
         super().__init__()
@@ -510,23 +591,35 @@ class FP8SwiGLU(nn.Module):
             raise ValueError("gate_up must have twice down's in_features outputs")
         self.gate_up, self.down = gate_up, down
 
+    def fused(self) -> bool:
+        """Whether the gate+up GEMM applies SwiGLU in its epilogue (the
+        intermediate size a multiple of 16, the hidden size at most 16384)."""
+        return self.down.in_features % 16 == 0 and self.gate_up.in_features <= QUANT_MAX_PACKED_COLS
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shape = x.shape
-        gu = self.gate_up(x.reshape(-1, shape[-1]))
-        M = gu.shape[0]
-        inter = self.down.in_features
+        x2 = x.reshape(-1, shape[-1])
+        M, inter = x2.shape[0], self.down.in_features
         if self.down.activations == "bf16":
             # W8A16 parity mode: h = silu(gate) * up in bf16 feeds the down GEMM as is.
+            gu = self.gate_up(x2)
             h = swiglu_quantize(gu[:, :inter], gu[:, inter:], return_h=True)[-1]
             w, tiled = self.down.kernel_weight()
             y = fp8_matmul_w8a16(h, w, self.down.scale, bias=self.down.bias, tiled=tiled)
             return y.view(*shape[:-1], self.down.out_features)
         lora_a = self.down.lora[0] if self.down.lora is not None else None
         # The down GEMM reads its codes fastest in fragment order (both the
-        # decode and the prefill kernels); the fused quantizer writes them so
-        # for rows up to 16384 channels.
+        # decode and the prefill kernels); the quantizers write them so for
+        # rows up to 16384 channels.
         packed = M > 0 and inter % BLOCK_K == 0 and inter <= QUANT_MAX_PACKED_COLS
-        out = swiglu_quantize(gu[:, :inter], gu[:, inter:], lora_a=lora_a, packed=packed)
+        if self.gate_up.activations == "fp8" and self.fused():
+            w, tiled = self.gate_up.kernel_weight()
+            h = gate_up_swiglu(x2.to(torch.bfloat16), w, self.gate_up.scale, bias=self.gate_up.bias,
+                               lora=self.gate_up.lora, tiled=tiled)
+            out = quantize_swiglu_output(h, lora_a=lora_a, packed=packed)
+        else:
+            gu = self.gate_up(x2)
+            out = swiglu_quantize(gu[:, :inter], gu[:, inter:], lora_a=lora_a, packed=packed)
         lora_t = out[2] if lora_a is not None else None
         w, tiled = self.down.kernel_weight()
         y = fp8_matmul_quantized(out[0], out[1], w, self.down.scale, bias=self.down.bias, lora_t=lora_t,

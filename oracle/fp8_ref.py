@@ -165,8 +165,15 @@ def quantize_rows(weight: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     w = np.ascontiguousarray(weight, dtype=np.float32)
     if w.ndim != 2:
         raise ValueError("quantize_rows takes a 2-D array")
+    rows, cols = w.shape
+    # Rows are independent: large inputs go in blocks of about 1M elements so
+    # the encoder's temporaries stay small (same result as one pass).
+    block = max(1, (1 << 20) // max(cols, 1))
+    if rows > block:
+        parts = [quantize_rows(w[r:r + block]) for r in range(0, rows, block)]
+        return np.concatenate([c for c, _ in parts]), np.concatenate([s for _, s in parts])
     with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
-        amax = np.max(np.abs(w), axis=1) if w.shape[1] else np.zeros(w.shape[0], np.float32)
+        amax = np.max(np.abs(w), axis=1) if cols else np.zeros(rows, np.float32)
         scale = (np.maximum(amax, SCALE_CLAMP_MIN) * FP8_MAX_RECIPROCAL).astype(np.float32)
         q = (w / scale[:, None]).astype(np.float32)
     return e4m3_encode(q), scale
