@@ -41,14 +41,48 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
 }
 
+// silu(g) = g / (1 + exp(-g)) for a bf16 g, in the form the epilogues can
+// afford: exp(-g) as the hardware 2^x of -g log2(e) (v_exp_f32), and for
+// |g| < 64 the quotient from the hardware reciprocal with Markstein's
+// correction (one product, two FMAs; the sign put back for -0), the IEEE
+// division beyond. Rounded to bf16 it equals torch's float32 silu rounded to
+// bf16 for every one of the 65536 bf16 inputs (checked exhaustively on the
+// device by the conformance tests), so it is exact where it is used.
+__device__ __forceinline__ float silu_of_bf16(float g) {
+  const float d = 1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+  if (__builtin_fabsf(g) < 64.0f) {
+    const float r = __builtin_amdgcn_rcpf(d);
+    const float q0 = g * r;
+    const float e = __builtin_fmaf(-q0, d, g);
+    return __builtin_copysignf(__builtin_fmaf(e, r, q0), g);
+  }
+  return g / d;
+}
+
 // SwiGLU on bf16 values (SwiGLU.forward, model/model.py:583, as torch runs it
-// on bf16 tensors): silu(g) = g / (1 + exp(-g)) in fp32 rounded to bf16, times
-// up (exact in fp32), rounded to bf16.
+// on bf16 tensors): silu(g) rounded to bf16, times up (exact in fp32), rounded
+// to bf16.
 __device__ __forceinline__ uint32_t swiglu_bf16(uint32_t g16, uint32_t u16) {
-  const float g = bf16_to_f32(g16);
-  const float s = g / (1.0f + expf(-g));
-  const float sb = bf16_to_f32(f32_to_bf16(s));
+  const float sb = bf16_to_f32(f32_to_bf16(silu_of_bf16(bf16_to_f32(g16))));
   return f32_to_bf16(sb * bf16_to_f32(u16));
+}
+
+// SwiGLU of two channels from their fp32 gate and up values before the GEMM's
+// bf16 rounding: h0 in the low half, bitwise
+// swiglu_bf16(f32_to_bf16(g0), f32_to_bf16(u0)) (and likewise h1). The
+// roundings go two at a time through v_cvt_pk_bf16_f32 (equal to f32_to_bf16
+// on every non-NaN; a NaN stays a NaN), and a NaN h is canonicalised to
+// 0x7FC0 as f32_to_bf16 gives it.
+__device__ __forceinline__ uint32_t swiglu_pair_f32(float g0, float g1, float u0, float u1) {
+  const uint32_t gb = pack_bf16x2(g0, g1), ub = pack_bf16x2(u0, u1);
+  const float s0 = silu_of_bf16(__uint_as_float(gb << 16)), s1 = silu_of_bf16(__uint_as_float(gb & 0xFFFF0000u));
+  const uint32_t sb = pack_bf16x2(s0, s1);
+  const float h0 = __uint_as_float(sb << 16) * __uint_as_float(ub << 16);
+  const float h1 = __uint_as_float(sb & 0xFFFF0000u) * __uint_as_float(ub & 0xFFFF0000u);
+  uint32_t hb = pack_bf16x2(h0, h1);
+  if (h0 != h0) hb = (hb & 0xFFFF0000u) | 0x7FC0u;
+  if (h1 != h1) hb = (hb & 0x0000FFFFu) | 0x7FC00000u;
+  return hb;
 }
 
 // ---------------------------------------------------------------------------

@@ -254,27 +254,28 @@ __device__ __forceinline__ void store_tile_sw(uint8_t* lds, const float* scale_l
         const float4 sg = *reinterpret_cast<const float4*>(scale_lds + BM + cb + o);
         const float4 su = *reinterpret_cast<const float4*>(scale_lds + BM + cb + 16 + o);
         const float swg[4] = {sg.x, sg.y, sg.z, sg.w}, swu[4] = {su.x, su.y, su.z, su.w};
-        uint32_t hv[4];
+        float vg[4], vu[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float vg = (acc[j][i][4 * q + e] * sxm[i]) * swg[e];
-          float vu = (acc[j][i][4 * (q + 2) + e] * sxm[i]) * swu[e];
+          vg[e] = (acc[j][i][4 * q + e] * sxm[i]) * swg[e];
+          vu[e] = (acc[j][i][4 * (q + 2) + e] * sxm[i]) * swu[e];
           if constexpr (RANK > 0) {
-            vg += lora[4 * q + e] * ep.lora_scale;
-            vu += lora[4 * (q + 2) + e] * ep.lora_scale;
+            vg[e] += lora[4 * q + e] * ep.lora_scale;
+            vu[e] += lora[4 * (q + 2) + e] * ep.lora_scale;
           }
           if (ep.bias) {
             const int c = min(n0 + cb + o + e, N - 1);
-            vg = with_bias(ep, vg, bf16_to_f32(ep.bias[swiglu_channel(c, ep.half)]));
-            vu = with_bias(ep, vu, bf16_to_f32(ep.bias[swiglu_channel(c + 16, ep.half)]));
+            vg[e] = with_bias(ep, vg[e], bf16_to_f32(ep.bias[swiglu_channel(c, ep.half)]));
+            vu[e] = with_bias(ep, vu[e], bf16_to_f32(ep.bias[swiglu_channel(c + 16, ep.half)]));
           }
-          hv[e] = swiglu_bf16(f32_to_bf16(vg), f32_to_bf16(vu));
-          mx = max(mx, hv[e] & 0x7FFFu);
         }
+        const uint32_t h01 = swiglu_pair_f32(vg[0], vg[1], vu[0], vu[1]);
+        const uint32_t h23 = swiglu_pair_f32(vg[2], vg[3], vu[2], vu[3]);
+        if (ep.parts)
+          mx = max(max(mx, max(h01 & 0x7FFFu, (h01 >> 16) & 0x7FFFu)), max(h23 & 0x7FFFu, (h23 >> 16) & 0x7FFFu));
         const int hl = cb / 2 + o;  // h channel within the tile
         const int chunk = (hl >> 3) ^ (ml % OUT_CH);
-        *reinterpret_cast<uint2*>(lds + ml * (HBN * 2) + chunk * 16 + (hl & 4) * 2) =
-            uint2{hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16)};
+        *reinterpret_cast<uint2*>(lds + ml * (HBN * 2) + chunk * 16 + (hl & 4) * 2) = uint2{h01, h23};
       }
       if (ep.parts) {
         // blocks past the last h channel (a ragged last tile) have no slot

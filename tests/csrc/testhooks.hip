@@ -8,7 +8,8 @@
 //   * th_quotient_sweep: every (bf16 x, bf16 row maximum) pair through the
 //     quantizer's fast quotient + hardware encode vs IEEE division + spec encode;
 //   * th_mfma32 / th_mfma16: one FP8 MFMA on lane-supplied operands, to check
-//     the output lane layout the GEMM epilogues assume.
+//     the output lane layout the GEMM epilogues assume;
+//   * th_silu_sweep: the epilogues' silu on every bf16 input.
 #include <stdint.h>
 
 #include "fp8_common.h"
@@ -107,9 +108,20 @@ __global__ void mfma16_kernel(const i32x8* a, const i32x8* b, f32x4* d) {
   d[l] = mfma_16x16x128_fp8(a[l], b[l], f32x4{0.f, 0.f, 0.f, 0.f});
 }
 
+// swiglu_bf16(g, 1.0) = bf16(silu(g)) for every bf16 pattern g (one thread each).
+__global__ void silu_sweep_kernel(uint16_t* out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < 65536) out[i] = (uint16_t)swiglu_bf16((uint32_t)i, 0x3F80u);
+}
+
 }  // namespace
 
 extern "C" {
+
+int th_silu_sweep(uint16_t* out, void* stream) {
+  silu_sweep_kernel<<<dim3(256), dim3(256), 0, (hipStream_t)stream>>>(out);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
 
 int th_encode(const float* in, uint8_t* hw, uint8_t* sw, int64_t n, void* stream) {
   if (n <= 0) return 0;

@@ -56,6 +56,19 @@ def test_hardware_encoder_equals_spec_on_whole_domain(hooks_lib):
     print(f"hardware vs spec encoder outside |f|<=449: {int(rest[1])} differing positive patterns")
 
 
+def test_silu_exhaustive_on_device(hooks_lib):
+    """The epilogues' silu (hardware exp2, Markstein-corrected reciprocal for
+    |g| < 64, IEEE division beyond) rounded to bf16 equals torch's float32
+    silu rounded to bf16 (the oracle's silu_f32, pinned to torch on all 65536
+    inputs) for every bf16 gate value, NaN positions included."""
+    out = torch.empty(65536, dtype=torch.int16, device="cuda")
+    assert hooks_lib.th_silu_sweep(out.data_ptr(), helpers.stream()) == 0
+    got = out.cpu().numpy().view(np.uint16)
+    g = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = oracle.f32_to_bf16(oracle.silu_f32(oracle.bf16_to_f32(g)))
+    assert oracle.bitwise_equal_fraction(got, want) == 1.0
+
+
 def test_fast_quotient_exhaustive_on_device(hooks_lib):
     counts = torch.zeros(3, dtype=torch.int64, device="cuda")
     first = torch.full((1,), -1, dtype=torch.int32, device="cuda")
