@@ -64,20 +64,25 @@ LAUNCHES_PER_GRAPH = 24
 # to a power of two, inference/engine.py:299-306).
 DECODE_SWEEP_ROWS = (1, 4, 32, 64, 96, 128)
 PREFILL_SWEEP_ROWS = (512, 8192)
-PMC_SUMMARY = "profiles/gate_up_hbm_traffic_pmc.md"
+PMC_SUMMARY = "profiles/gemm_decode_prefill_pmc.md"
 
 
-def measured_traffic(key: str):
-    """HBM bytes per launch measured with rocprofv3 PMC counters, copied from
-    the committed summary (None when absent)."""
+def measured_counter(kind: str, key: str):
+    """A per-launch figure measured with rocprofv3 PMC counters (HBM bytes,
+    MFMA busy %, counter-window clock), copied from the committed summary
+    (None when absent)."""
     path = ROOT / PMC_SUMMARY
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
         parts = line.split()
-        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == key:
-            return int(parts[2])
+        if len(parts) == 3 and parts[0] == kind and parts[1] == key:
+            return int(parts[2]) if kind == "traffic_bytes_per_launch" else float(parts[2])
     return None
+
+
+def measured_traffic(key: str):
+    return measured_counter("traffic_bytes_per_launch", key)
 
 
 def linear_bytes(M: int, N: int, K: int) -> int:
@@ -369,28 +374,40 @@ def cpu_baseline(synthetic, M: int, budget_s: float) -> dict:
             **host_description()}
 
 
-def pmc_driver(torch, fp8, synthetic, quantize_rows, launches: int = 10) -> None:
-    """Workload for the hardware-counter runs (rocprofv3 --pmc FETCH_SIZE, then
-    WRITE_SIZE): a 256 MiB device copy of known size (reads and writes 256 MiB;
-    it calibrates the counters), then `launches` launches each of the gate+up
-    decode GEMM (M=16, packed codes) and the gate+up prefill GEMM (M=2048),
-    each on a fresh weight copy, one launch per dispatch record."""
+def pmc_driver(torch, fp8, synthetic, quantize_rows, launches: int = 6) -> None:
+    """Workload for the hardware-counter runs (rocprofv3 --pmc, one counter set
+    per run): a 256 MiB device copy of known size (reads and writes 256 MiB;
+    it calibrates FETCH_SIZE and WRITE_SIZE), then `launches` GEMM launches of
+    every decode shape at M=16 (q, k, v, o, gate+up, down and the merged
+    q/k/v) and of the prefill shapes at M=2048 (q, k, gate+up, down, merged
+    q/k/v, and gate+up with the SwiGLU epilogue), each on one of four weight
+    copies in the tiled layout, each launch one dispatch record. The GEMMs run
+    on activations quantized beforehand (the SwiGLU launches include their
+    quantizer)."""
     copy_src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
     copy_dst = torch.empty_like(copy_src)
     copy_dst.copy_(copy_src)
     torch.cuda.synchronize()
-    for M, case in ((16, synthetic.decode_case), (2048, synthetic.prefill_case)):
-        x, w = case("gate_up", M)
-        x = x.cuda()
-        wq, sw = quantize_rows(w.cuda())
-        wq = fp8.tile_weight(wq)
-        ops = quantized_operands(torch, fp8, x)
-        copies = [wq] + [wq.clone() for _ in range(3)]
-        torch.cuda.synchronize()
-        for i in range(launches):
-            fp8.fp8_matmul_quantized(ops[0], ops[1], copies[i % len(copies)], sw, packed_rows=ops[2], tiled=True)
-        torch.cuda.synchronize()
-        del copies
+    weights = make_weights(torch, synthetic, quantize_rows)
+    del copy_src, copy_dst
+    for M, case, names in ((16, synthetic.decode_case, ("q", "k", "v", "o", "gate_up", "down", "qkv")),
+                           (2048, synthetic.prefill_case, ("q", "k", "gate_up", "down", "qkv"))):
+        for name in names:
+            wq, sw = weights[name]
+            x = case("q" if name == "qkv" else name, M)[0].cuda()
+            ops = quantized_operands(torch, fp8, x)
+            copies = [wq] + [wq.clone() for _ in range(3)]
+            torch.cuda.synchronize()
+            for i in range(launches):
+                fp8.fp8_matmul_quantized(ops[0], ops[1], copies[i % len(copies)], sw, packed_rows=ops[2], tiled=True)
+            torch.cuda.synchronize()
+            del copies
+    x = synthetic.prefill_case("gate_up", 2048)[0].cuda()
+    wq, sw = weights["gate_up"]
+    copies = [wq] + [wq.clone() for _ in range(3)]
+    for i in range(launches):
+        fp8.gate_up_swiglu(x, copies[i % len(copies)], sw, tiled=True)
+    torch.cuda.synchronize()
     print("pmc driver done", flush=True)
 
 
@@ -640,7 +657,11 @@ def main() -> int:
                          "frac": round(pk_tf / FP8_PEAK_TFLOPS, 4), "avg_launch_us": round(pk_us, 2),
                          "traffic": measured_traffic(f"prefill_gate_up_m{Mp}"),
                          "traffic_source": f"copied from {PMC_SUMMARY}, not measured in this run",
-                         "flops_per_launch": 2 * Mp * N * Kg},
+                         "flops_per_launch": 2 * Mp * N * Kg,
+                         "mfma_busy_pct": measured_counter("mfma_busy_pct", f"prefill_gate_up_m{Mp}"),
+                         "window_clock_ghz": measured_counter("window_clock_ghz", f"prefill_gate_up_m{Mp}"),
+                         "counters_source": f"copied from {PMC_SUMMARY} (SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE), "
+                                            "not measured in this run"},
             "kernels": pk,
             "kernels_sweep": psweep,
         }
