@@ -9,7 +9,11 @@
 //     quantizer's fast quotient + hardware encode vs IEEE division + spec encode;
 //   * th_mfma32 / th_mfma16: one FP8 MFMA on lane-supplied operands, to check
 //     the output lane layout the GEMM epilogues assume;
-//   * th_silu_sweep: the epilogues' silu on every bf16 input.
+//   * th_silu_sweep: the epilogues' silu on every bf16 input;
+//   * th_gemm_form: a plain FP8 GEMM, one wave per output tile, through one of
+//     gfx950's FP8 MFMA forms (the two f8f6f4 forms the product kernels use and
+//     the older 32x32x16 / 16x16x32 fp8_fp8 forms), to compare their
+//     accumulation with the exact product.
 #include <stdint.h>
 
 #include "fp8_common.h"
@@ -114,9 +118,70 @@ __global__ void silu_sweep_kernel(uint16_t* out) {
   if (i < 65536) out[i] = (uint16_t)swiglu_bf16((uint32_t)i, 0x3F80u);
 }
 
+// Form 0: 32x32x64 f8f6f4, 1: 16x16x128 f8f6f4, 2: 32x32x16 fp8_fp8,
+// 3: 16x16x32 fp8_fp8. Weights are the A operand (channels = output rows),
+// tokens the B operand; lane l loads row l % T of each at k byte
+// (l / T) * BYTES of the instruction's k range. y = bf16((acc * sx[m]) * sw[n]),
+// or, with sx null, the fp32 sums themselves (y then holds floats).
+template <int FORM>
+__global__ void gemm_form_kernel(const uint8_t* w, const float* sw, const uint8_t* x, const float* sx, uint16_t* y, int N,
+                                 int K) {
+  constexpr int T = (FORM == 0 || FORM == 2) ? 32 : 16;
+  constexpr int BYTES = FORM < 2 ? 32 : 8;
+  constexpr int KI = BYTES * (64 / T);
+  constexpr int REGS = T * T / 64;
+  typedef float facc __attribute__((ext_vector_type(REGS)));
+  const int l = threadIdx.x;
+  const int n0 = blockIdx.x * T, m0 = blockIdx.y * T;
+  const uint8_t* wr = w + (int64_t)(n0 + l % T) * K + (l / T) * BYTES;
+  const uint8_t* xr = x + (int64_t)(m0 + l % T) * K + (l / T) * BYTES;
+  facc acc;
+  for (int r = 0; r < REGS; ++r) acc[r] = 0.0f;
+  for (int k = 0; k < K; k += KI) {
+    if constexpr (FORM == 0) {
+      acc = mfma_32x32x64_fp8(*reinterpret_cast<const i32x8*>(wr + k), *reinterpret_cast<const i32x8*>(xr + k), acc);
+    } else if constexpr (FORM == 1) {
+      acc = mfma_16x16x128_fp8(*reinterpret_cast<const i32x8*>(wr + k), *reinterpret_cast<const i32x8*>(xr + k), acc);
+    } else if constexpr (FORM == 2) {
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(*reinterpret_cast<const long*>(wr + k),
+                                                       *reinterpret_cast<const long*>(xr + k), acc, 0, 0, 0);
+    } else {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(*reinterpret_cast<const long*>(wr + k),
+                                                       *reinterpret_cast<const long*>(xr + k), acc, 0, 0, 0);
+    }
+  }
+  for (int r = 0; r < REGS; ++r) {
+    const int n = n0 + (T == 32 ? 8 * (r / 4) + 4 * (l / 32) + r % 4 : 4 * (l / 16) + r);
+    const int m = m0 + l % T;
+    if (sx)
+      y[(int64_t)m * N + n] = (uint16_t)f32_to_bf16((acc[r] * sx[m]) * sw[n]);
+    else
+      reinterpret_cast<float*>(y)[(int64_t)m * N + n] = acc[r];
+  }
+}
+
 }  // namespace
 
 extern "C" {
+
+// M and N multiples of the form's tile (32 or 16), K of its k range (64, 128,
+// 16 or 32 bytes); 1 when they are not. With sx null, y receives M x N fp32
+// sums (sw unused).
+int th_gemm_form(int form, const uint8_t* w, const float* sw, const uint8_t* x, const float* sx, uint16_t* y, int M,
+                 int N, int K, void* stream) {
+  if (form < 0 || form > 3 || M <= 0 || N <= 0 || K <= 0) return 1;
+  const int T = (form == 0 || form == 2) ? 32 : 16;
+  const int KI = (form < 2 ? 32 : 8) * (64 / T);
+  if (M % T || N % T || K % KI) return 1;
+  const dim3 grid((unsigned)(N / T), (unsigned)(M / T)), block(64);
+  hipStream_t s = (hipStream_t)stream;
+  if (form == 0) gemm_form_kernel<0><<<grid, block, 0, s>>>(w, sw, x, sx, y, N, K);
+  else if (form == 1) gemm_form_kernel<1><<<grid, block, 0, s>>>(w, sw, x, sx, y, N, K);
+  else if (form == 2) gemm_form_kernel<2><<<grid, block, 0, s>>>(w, sw, x, sx, y, N, K);
+  else gemm_form_kernel<3><<<grid, block, 0, s>>>(w, sw, x, sx, y, N, K);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
 
 int th_silu_sweep(uint16_t* out, void* stream) {
   silu_sweep_kernel<<<dim3(256), dim3(256), 0, (hipStream_t)stream>>>(out);

@@ -34,8 +34,9 @@ def hooks() -> ctypes.CDLL:
         h.th_mfma16.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p]
         h.th_mfma32_acc.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
         h.th_silu_sweep.argtypes = [c_void_p, c_void_p]
+        h.th_gemm_form.argtypes = [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]
         for f in (h.th_encode, h.th_encode_sweep, h.th_quotient_sweep, h.th_mfma32, h.th_mfma16, h.th_mfma32_acc,
-                  h.th_silu_sweep):
+                  h.th_silu_sweep, h.th_gemm_form):
             f.restype = c_int
         _hooks = h
     return _hooks

@@ -117,5 +117,5 @@ def test_packed_layout_sizes_are_host_logic(product_lib):
 
 
 def test_hook_library_exports(hooks_lib):
-    for name in ("th_encode", "th_encode_sweep", "th_quotient_sweep", "th_mfma32", "th_mfma16", "th_silu_sweep"):
+    for name in ("th_encode", "th_encode_sweep", "th_quotient_sweep", "th_mfma32", "th_mfma16", "th_silu_sweep", "th_gemm_form"):
         assert hasattr(hooks_lib, name)
