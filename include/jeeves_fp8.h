@@ -75,6 +75,15 @@ int64_t jv_fp8_packed_codes_bytes(int64_t rows, int64_t cols);
 int jv_fp8_quantize_rows_f32(const float* x, int64_t ldx, int64_t rows, int64_t cols, void* codes, int64_t ldc,
                              float* scales, void* stream);
 
+/* quantize_rows on the host CPU (inference/fp8_weights.py:16-19), for the
+ * exporter's quantize_row_blocks_on_cpu (inference/fp8_weights.py:22-26) on
+ * a machine without a GPU: float32 rows in, e4m3 codes [rows, cols] (row
+ * stride ldc) and float32 scales [rows] out, bitwise equal to the device
+ * quantizer. Runs on `threads` host threads (0: all hardware threads); makes
+ * no HIP call. */
+int jv_fp8_quantize_rows_host(const float* w, int64_t ldw, int64_t rows, int64_t cols, void* codes, int64_t ldc,
+                              float* scales, int threads);
+
 /* Workspace bytes jv_fp8_linear needs for these sizes (activation codes and
  * scales, LoRA low-rank activations, split-K partials). */
 int64_t jv_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t lora_rank);

@@ -21,6 +21,7 @@ SIGNATURES: dict[str, tuple] = {
     "jv_device_cu_count": (c_int, [c_int]),
     "jv_fp8_quantize_rows_bf16": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
     "jv_fp8_quantize_rows_f32": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
+    "jv_fp8_quantize_rows_host": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int]),
     "jv_fp8_packed_codes_bytes": (c_int64, [c_int64, c_int64]),
     "jv_fp8_linear_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
     "jv_fp8_linear": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_float,

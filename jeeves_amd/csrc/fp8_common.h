@@ -90,11 +90,11 @@ __device__ __forceinline__ uint32_t swiglu_pair_f32(float g0, float g1, float u0
 // Written from the OCP FP8 v1.0 format definition; this is the semantics of
 // torch's float -> float8_e4m3fn cast that the reference quantizer uses.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t e4m3_encode_sw(float f) {
-  const uint32_t b = __float_as_uint(f);
+__host__ __device__ __forceinline__ uint32_t e4m3_encode_sw(float f) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, f);
   const uint32_t sign = (b >> 24) & 0x80u;
   const uint32_t mb = b & 0x7FFFFFFFu;
-  const float mag = __uint_as_float(mb);
+  const float mag = __builtin_bit_cast(float, mb);
   uint32_t code;
   if (!(mag <= 464.0f)) {
     code = 0x7Fu;

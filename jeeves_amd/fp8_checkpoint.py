@@ -35,7 +35,8 @@ def quantized_linears(module: nn.Module) -> set[str]:
 
 def quantize_on_cpu(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """CPU weight in, CPU ``(codes, scale)`` out, quantized in row blocks
-    (``inference/fp8_checkpoint.py:30-35``; each block runs on the HIP device)."""
+    (``inference/fp8_checkpoint.py:30-35``; each block runs on the HIP device,
+    or on the host quantizer where there is none)."""
     codes = torch.empty(weight.shape, dtype=FP8)
     scale = torch.empty(weight.shape[0], dtype=torch.float32)
     for rows, block_codes, block_scale in quantize_row_blocks_on_cpu(weight):

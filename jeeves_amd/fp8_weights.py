@@ -4,9 +4,13 @@ quantizer, the quantizability rule and module replacement.
 ``quantize_rows`` computes the reference's arithmetic
 (``inference/fp8_weights.py:16-19``) with the gfx950 quantizer kernel
 (``jeeves_amd/csrc/quant.hip``) and returns the same codes and scales bit for
-bit. It runs on the HIP device; tensors on the CPU are moved to the current
-HIP device for the kernel and the results moved back, so the exporter's
-``quantize_row_blocks_on_cpu`` keeps its CPU-in, CPU-out contract.
+bit. It runs on the HIP device (tensors on the CPU are moved to the current
+HIP device for the kernel and the results moved back) and raises when there
+is none. The exporter's ``quantize_row_blocks_on_cpu`` keeps the reference's
+CPU-in, CPU-out contract: it uses the HIP quantizer when a device is present
+and otherwise the library's host quantizer
+(``jeeves_amd/csrc/quant_host.hip``, the same bits), so an FP8 checkpoint can
+be exported on a machine without a GPU, as the reference's exporter is.
 """
 
 from __future__ import annotations
@@ -34,6 +38,25 @@ def _hip_device(t: torch.Tensor) -> torch.device:
     return torch.device("cuda", torch.cuda.current_device())
 
 
+def quantize_rows_host(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """quantize_rows of a CPU tensor on the host CPU, with the library's host
+    quantizer (``jv_fp8_quantize_rows_host``): the same codes and scales as the
+    HIP quantizer, on torch's intra-op thread count."""
+    w = weight.detach()
+    if w.dim() != 2:
+        raise ValueError(f"quantize_rows takes a 2-D tensor, got shape {tuple(w.shape)}")
+    if w.shape[0] and not w.shape[1]:
+        raise ValueError("quantize_rows needs at least one column")
+    src = w.cpu().float().contiguous()
+    rows, cols = src.shape
+    codes = torch.empty(rows, cols, dtype=torch.uint8)
+    scale = torch.empty(rows, dtype=torch.float32)
+    if rows:
+        _lib.check(_lib.lib().jv_fp8_quantize_rows_host(src.data_ptr(), cols, rows, cols, codes.data_ptr(), cols,
+                                                         scale.data_ptr(), torch.get_num_threads()))
+    return codes.view(FP8), scale
+
+
 def quantize_rows(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-row e4m3fn quantization (``inference/fp8_weights.py:16-19``).
 
@@ -47,6 +70,9 @@ def quantize_rows(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     home = w.device
     dev = _hip_device(w)
     rows, cols = w.shape
+    if rows and not cols:
+        # No columns: amax over an empty row is undefined in the reference too.
+        raise ValueError("quantize_rows needs at least one column")
     codes = torch.empty(rows, cols, dtype=torch.uint8, device=dev)
     scale = torch.empty(rows, dtype=torch.float32, device=dev)
     if rows and cols:
@@ -69,9 +95,6 @@ def quantize_rows(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
                                                                 scale.data_ptr(), stream))
                 if out is not codes:
                     codes.copy_(out[:, :cols])
-    elif rows:
-        # No columns: amax over an empty row is undefined in the reference too.
-        raise ValueError("quantize_rows needs at least one column")
     codes = codes.view(FP8)
     if home != dev:
         codes, scale = codes.to(home), scale.to(home)
@@ -80,10 +103,13 @@ def quantize_rows(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
 def quantize_row_blocks_on_cpu(weight: torch.Tensor) -> Iterator[tuple[slice, torch.Tensor, torch.Tensor]]:
     """``inference/fp8_weights.py:22-26``: quantize in blocks of rows, CPU tensors
-    out. Each block goes through the HIP quantizer."""
+    out. Each block goes through the HIP quantizer, or the host quantizer on a
+    machine without a HIP device (the reference quantizes these blocks on the
+    CPU; both give its bits)."""
+    quantize = quantize_rows if torch.cuda.is_available() else quantize_rows_host
     for start in range(0, weight.shape[0], QUANTIZE_BLOCK_ROWS):
         rows = slice(start, start + QUANTIZE_BLOCK_ROWS)
-        codes, scale = quantize_rows(weight[rows])
+        codes, scale = quantize(weight[rows])
         yield rows, codes.cpu(), scale.cpu()
 
 

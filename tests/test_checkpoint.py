@@ -1,9 +1,11 @@
 """FP8 checkpoint format (inference/fp8_checkpoint.py:26-85, export_fp8.py:15-44)
 on the host: the writer keeps every non-linear tensor, replaces each quantized
 linear's weight by e4m3 codes plus a float32 `<name>.weight_scale`, and the
-loader puts codes and scales back into FP8Linear buffers bit for bit. The
-quantizer itself runs on the GPU; here the oracle's restatement stands in
-for it (the GPU round trip is tests/test_gpu_checkpoint.py)."""
+loader puts codes and scales back into FP8Linear buffers bit for bit. Most
+tests pass the oracle's restatement as the quantizer; the export test runs the
+product's own path on this GPU-less host (the library's host quantizer), as the
+reference's exporter runs on the CPU (the GPU round trip is
+tests/test_gpu_checkpoint.py)."""
 
 from __future__ import annotations
 
@@ -114,8 +116,10 @@ def test_load_tensors_reports_unused_keys_and_bad_shapes(tmp_path):
     assert unexpected == []
 
 
-def test_export_layout(tmp_path, monkeypatch):
-    monkeypatch.setattr(fp8_checkpoint, "quantize_on_cpu", oracle_quantize)
+@pytest.mark.skipif(torch.cuda.is_available(), reason="exercises the exporter on a host without a GPU")
+def test_export_layout(tmp_path):
+    """export_fp8 end to end on a host without a GPU: the quantized tensors are
+    the oracle's codes and scales bit for bit."""
     src, out = tmp_path / "export", tmp_path / "fp8"
     src.mkdir()
     make_checkpoint(src / "model-00001-of-00002.safetensors", 1)
@@ -137,5 +141,11 @@ def test_export_layout(tmp_path, monkeypatch):
     assert index["metadata"]["total_size"] > 0
     with safe_open(str(out / "drafter.safetensors"), framework="pt", device="cpu") as fh:
         assert fh.get_tensor("delta_q.weight").dtype == FP8
+    source = make_checkpoint(tmp_path / "again.safetensors", 1)
+    with safe_open(str(out / "model-00001-of-00002.safetensors"), framework="pt", device="cpu") as fh:
+        for name in ("q", "o"):
+            want_codes, want_scale = oracle_quantize(source[f"{name}.weight"])
+            assert torch.equal(fh.get_tensor(f"{name}.weight").view(torch.uint8), want_codes.view(torch.uint8)), name
+            assert torch.equal(fh.get_tensor(f"{name}.weight" + SCALE_SUFFIX), want_scale), name
     with pytest.raises(FileExistsError):
         export_fp8.main([str(src), "--out", str(out), "--linears", str(linears)])

@@ -1,6 +1,7 @@
 """Host-side logic of the drop-in module that runs without a GPU: the
 quantizability rule, module replacement, FP8Linear buffers and merges,
-argument validation, and the synthetic workload generators."""
+argument validation, the host quantizer of GPU-less exports, and the
+synthetic workload generators."""
 
 from __future__ import annotations
 
@@ -10,7 +11,9 @@ import torch
 import torch.nn as nn
 
 import jeeves_amd
+import oracle
 from jeeves_amd import synthetic
+from tests import helpers
 from jeeves_amd.fp8 import FP8Linear, fp8_matmul
 from jeeves_amd.fp8_weights import FP8, FP8_MAX, FP8_MAX_RECIPROCAL, QUANTIZE_BLOCK_ROWS, SCALE_SUFFIX, quantizable, replace_linears
 
@@ -179,3 +182,65 @@ def test_decode_case_seeds_are_distinct():
     xb, wb = synthetic.decode_case("o", 16)
     assert torch.equal(xa, xb) and not torch.equal(wa, wb)
     assert np.isfinite(xa.float().numpy()).all()
+
+
+def test_host_quantizer_matches_golden_fixtures_and_oracle():
+    """The library's host quantizer (the exporter's path on a machine without a
+    GPU) against torch's own quantize_rows outputs (tests/golden) and the
+    oracle on rows with zeros, subnormals, huge values, inf and NaN, on 1 and
+    several threads."""
+    from jeeves_amd import _lib
+
+    L = _lib.lib()
+
+    def host(w: np.ndarray, threads: int):
+        w = np.ascontiguousarray(w, np.float32)
+        rows, cols = w.shape
+        codes = np.empty((rows, cols), np.uint8)
+        scales = np.empty(rows, np.float32)
+        _lib.check(L.jv_fp8_quantize_rows_host(w.ctypes.data, cols, rows, cols, codes.ctypes.data, cols,
+                                               scales.ctypes.data, threads))
+        return codes, scales
+
+    g = helpers.golden("quantize_rows.npz")
+    for name in ("edge", "cfg0_x", "cfg0_w64"):
+        x = g[f"{name}_x" if name == "edge" else name]
+        codes, scales = host(oracle.bf16_to_f32(x), 3)
+        want_codes = g[f"{name}_codes"]
+        nan = (want_codes & 0x7F) == 0x7F
+        assert np.array_equal(codes[~nan], want_codes[~nan]) and np.all((codes[nan] & 0x7F) == 0x7F), name
+        assert np.array_equal(scales.view(np.uint32), g[f"{name}_scales"].view(np.uint32)), name
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((257, 999)) * rng.choice([1e-40, 1e-30, 1e-3, 1.0, 1e4, 3e38], (257, 1))).astype(np.float32)
+    w[5, 3], w[6], w[7, 2], w[8], w[9, 1::2] = np.inf, 0.0, np.nan, -np.inf, 1e-45
+    want_codes, want_scales = oracle.quantize_rows(w)
+    for threads in (1, 4, 0):
+        codes, scales = host(w, threads)
+        assert np.array_equal(codes, want_codes.view(np.uint8)), threads
+        assert np.array_equal(scales.view(np.uint32), want_scales.view(np.uint32)), threads
+    # argument errors, no HIP call
+    bad = np.zeros((2, 4), np.float32)
+    out = np.zeros((2, 4), np.uint8)
+    sc = np.zeros(2, np.float32)
+    assert L.jv_fp8_quantize_rows_host(bad.ctypes.data, 2, 2, 4, out.ctypes.data, 4, sc.ctypes.data, 1) == 1
+    assert L.jv_fp8_quantize_rows_host(bad.ctypes.data, 4, 2, 0, out.ctypes.data, 4, sc.ctypes.data, 1) == 1
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="the path for hosts without a GPU")
+def test_quantize_row_blocks_on_cpu_without_a_gpu(monkeypatch):
+    """inference/fp8_weights.py:22-26 on a host without a GPU: CPU blocks in
+    order, bitwise the oracle's; quantize_rows itself still refuses to run
+    without a HIP device."""
+    from jeeves_amd import fp8_weights
+
+    monkeypatch.setattr(fp8_weights, "QUANTIZE_BLOCK_ROWS", 48)
+    w = (torch.randn(100, 256, generator=torch.Generator().manual_seed(3)) * 0.05).to(torch.bfloat16)
+    blocks = list(fp8_weights.quantize_row_blocks_on_cpu(w))
+    assert [b[0] for b in blocks] == [slice(0, 48), slice(48, 96), slice(96, 144)]
+    codes = torch.cat([b[1] for b in blocks]).view(torch.uint8).numpy()
+    scales = torch.cat([b[2] for b in blocks]).numpy()
+    want_codes, want_scales = oracle.quantize_rows(w.float().numpy())
+    assert all(b[1].device.type == "cpu" and b[1].dtype == fp8_weights.FP8 for b in blocks)
+    assert np.array_equal(codes, want_codes.view(np.uint8)) and np.array_equal(scales, want_scales)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        fp8_weights.quantize_rows(w)
