@@ -219,8 +219,10 @@ int jv_fp8_untile_weight(const void* tiled, int64_t N, int64_t K, void* codes, i
 
 /* Dispatch introspection (the role of split_for, inference/fp8.py:105-109):
  * the number of K splits across workgroups the GEMM uses for these sizes on a
- * device with cu_count compute units (1 = no cross-workgroup split), and the
- * tile counters it needs. */
+ * device with cu_count compute units (1 = no cross-workgroup split; the
+ * decode kernel splits narrow weights, the prefill tiles split K when too few
+ * of them fill the CUs, as the reference splits below 256 rows,
+ * inference/fp8.py:118-123), and the tile counters it needs. */
 int jv_fp8_split_for(int64_t M, int64_t N, int64_t K, int cu_count);
 int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count);
 

@@ -60,9 +60,11 @@ int64_t split_partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
   return s > 1 ? round_up((int64_t)s * M * N * 4, 256) : 0;
 }
 
-// The same for the fp8 GEMM's kernel choice (0 on the prefill kernel).
+// The same for the fp8 GEMM's kernel choice: decode split-K partials, or the
+// prefill tiles' split-K partial tiles.
 int64_t partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
-  return jv::decode_kernel_for(M, N, cus) ? split_partial_bytes(M, N, K, cus) : 0;
+  if (jv::decode_kernel_for(M, N, cus)) return split_partial_bytes(M, N, K, cus);
+  return round_up(jv::prefill_partial_bytes(jv::prefill_tile(M, N, K, cus), M, N), 256);
 }
 
 // Activation codes for jv_fp8_linear: the packed fragment order whenever the
@@ -100,8 +102,22 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, co
                                       stream),
                       "fp8 decode GEMM launch");
   }
-  const jv::PrefillTile tile = jv::prefill_tile(M, N, cus);
-  return hip_status(jv::gemm_prefill(xq, packed_x ? 0 : ldxq, w, ldw, (int)M, (int)N, (int)K, ep, (int)rank, tile, stream),
+  jv::PrefillTile tile = jv::prefill_tile(M, N, K, cus);
+  // The fused SwiGLU GEMM keeps whole k ranges (its callers pass no partials).
+  if (swiglu_half) tile.splits = 1;
+  float* partials = nullptr;
+  if (tile.splits > 1) {
+    const int64_t tiles = jv::prefill_counters(tile, M, N);
+    if (!counters || tiles > n_counters)
+      return fail(JV_ERR_VALUE, "%lld tiles exceed the %lld tile counters", (long long)tiles, (long long)n_counters);
+    const int64_t need = jv::prefill_partial_bytes(tile, M, N);
+    if (!partial_ws || partial_ws_bytes < need)
+      return fail(JV_ERR_VALUE, "workspace too small for split-K partials: %lld < %lld bytes", (long long)partial_ws_bytes,
+                  (long long)need);
+    partials = reinterpret_cast<float*>(partial_ws);
+  }
+  return hip_status(jv::gemm_prefill(xq, packed_x ? 0 : ldxq, w, ldw, (int)M, (int)N, (int)K, ep, (int)rank, tile, partials,
+                                     counters, stream),
                     "fp8 prefill GEMM launch");
 }
 
@@ -350,12 +366,14 @@ int jv_fp8_untile_weight(const void* tiled, int64_t N, int64_t K, void* codes, i
 }
 
 int jv_fp8_split_for(int64_t M, int64_t N, int64_t K, int cu_count) {
-  if (K <= 0 || N <= 0 || cu_count <= 0 || !jv::decode_kernel_for(M, N, cu_count)) return 1;
+  if (K <= 0 || N <= 0 || M <= 0 || cu_count <= 0) return 1;
+  if (!jv::decode_kernel_for(M, N, cu_count)) return jv::prefill_tile(M, N, K, cu_count).splits;
   return jv::decode_plan(M, N, K, cu_count).splits;
 }
 
 int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count) {
-  if (K <= 0 || N <= 0 || cu_count <= 0 || !jv::decode_kernel_for(M, N, cu_count)) return 0;
+  if (K <= 0 || N <= 0 || M <= 0 || cu_count <= 0) return 0;
+  if (!jv::decode_kernel_for(M, N, cu_count)) return jv::prefill_counters(jv::prefill_tile(M, N, K, cu_count), M, N);
   const jv::DecodePlan p = jv::decode_plan(M, N, K, cu_count);
   return p.splits > 1 ? p.groups : 0;
 }

@@ -308,11 +308,79 @@ __device__ __forceinline__ void store_tile_sw(uint8_t* lds, const float* scale_l
   }
 }
 
-template <int BM, int BN, int WGM, int WGN, int BK, int STAGES, int RANK, bool PACKW, bool PACKX, bool SW = false>
+// Split-K (splits > 1): workgroup tile + s * tiles adds up part s of the k
+// range (whole BK stages, split as evenly as they divide), writes its fp32
+// accumulators to its partial tile and counts in on the tile's counter; the
+// workgroup that counts last adds the partials of every split in split order
+// (its own from registers) and runs the epilogue, so the sum is the same
+// whichever workgroup finishes last, and resets the counter.
+// Ordering: the partials are written and read with device-scope atomic
+// stores and loads, which on gfx950 write through and read from the
+// device-coherent level past each XCD's L2; every wave's stores complete
+// (s_waitcnt vmcnt(0)) before the barrier that precedes the device-scope
+// count, and the last workgroup issues its loads after its count returned,
+// so they read completed partials. No cache-wide writeback or invalidation
+// (an agent-scope release/acquire pair) is needed on this path.
+constexpr int kMaxPrefillSplits = 8;
+
+template <int TN, int TM, int NW>
+__device__ __forceinline__ bool split_k_reduce(f32x16 (&acc)[TN][TM], float* __restrict__ partials,
+                                               int* __restrict__ counters, int tile, int split, int splits, int wave,
+                                               int lane, int* is_last) {
+  constexpr int Q = TN * TM * 16;  // floats per lane
+  const auto slot = [&](int s) { return partials + (((int64_t)tile * splits + s) * NW + wave) * Q * 64 + lane; };
+  float* mine = slot(split);
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        __hip_atomic_store(mine + ((j * TM + i) * 16 + r) * 64, acc[j][i][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *is_last = __hip_atomic_fetch_add(counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+  __syncthreads();
+  if (!*is_last) return false;
+  // One 32x32 block at a time: every other split's 16 values are loaded at
+  // once (all loads in flight together), then added in split order.
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int b = (j * TM + i) * 16;
+      float part[kMaxPrefillSplits][16];
+#pragma unroll
+      for (int s = 0; s < kMaxPrefillSplits; ++s)
+        if (s < splits && s != split) {
+          const float* p = slot(s);
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            part[s][r] = __hip_atomic_load(p + (b + r) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      f32x16 sum;
+#pragma unroll
+      for (int s = 0; s < kMaxPrefillSplits; ++s)
+        if (s < splits)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float v = s == split ? acc[j][i][r] : part[s][r];
+            sum[r] = s == 0 ? v : sum[r] + v;
+          }
+      acc[j][i] = sum;
+    }
+  if (threadIdx.x == 0) __hip_atomic_store(counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
+template <int BM, int BN, int WGM, int WGN, int BK, int STAGES, int RANK, bool PACKW, bool PACKX, bool SW = false,
+          bool SPLITK = false>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint8_t* __restrict__ xq, int64_t ldx,
                                                                       const uint8_t* __restrict__ w, int64_t ldw, int M,
                                                                       int N, int K, int tiles_m, int tiles_n, int group_m,
-                                                                      Epilogue ep) {
+                                                                      Epilogue ep, int splits, float* __restrict__ partials,
+                                                                      int* __restrict__ counters) {
   constexpr int NW = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;  // wave sub-tile: tokens x channels
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -328,13 +396,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
   constexpr int LDS_BYTES = STAGES * STAGE > BM * BN * 2 ? STAGES * STAGE : BM * BN * 2;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
   __shared__ __attribute__((aligned(256))) float scale_lds[BM + BN];  // sx of the tile's tokens, then sw of its channels
+  __shared__ int is_last;
 
+  const int tiles = tiles_m * tiles_n;
+  const int split = (int)blockIdx.x / tiles;
+  const int tile = (int)blockIdx.x - split * tiles;
   int tile_m, tile_n;
-  tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tile_m, tile_n);
+  tile_of(tile, tiles_m, tiles_n, group_m, tile_m, tile_n);
   const int m0 = tile_m * BM, n0 = tile_n * BN;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
 
   // Global -> LDS assignment. Wave-load g (g = i*NW + wave) fills LDS bytes
@@ -381,11 +453,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
     }
   }
 
+  // This workgroup's stages: [kt0, kt0 + KT) of the K / BK stages.
+  const int kt_all = K / BK;
+  const int kt0 = (int)((int64_t)kt_all * split / splits);
+  const int KT = (int)((int64_t)kt_all * (split + 1) / splits) - kt0;
   auto issue_stage = [&](int kt) {
     uint8_t* base = lds + (kt % STAGES) * STAGE;
-    const int64_t k0 = (int64_t)kt * BK;
-    const int64_t wk = PACKW ? tiled_stage_offset<BK>(kt) : k0;
-    const int64_t xk = PACKX ? tiled_stage_offset<BK>(kt) : k0;
+    const int ktg = kt0 + kt;
+    const int64_t k0 = (int64_t)ktg * BK;
+    const int64_t wk = PACKW ? tiled_stage_offset<BK>(ktg) : k0;
+    const int64_t xk = PACKX ? tiled_stage_offset<BK>(ktg) : k0;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) load_lds16(src[i] + (i * NW * RPL < BM ? xk : wk), base + (i * NW + wave) * 1024);
   };
@@ -420,7 +497,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
     __builtin_amdgcn_global_load_lds((global_void*)sp, (lds_void*)(scale_lds + t), 4, 0, 0);
   }
 
-  const int KT = K / BK;
   // Two fragment sets: while the MFMAs of 64-deep step u run on one set, the
   // LDS reads of step u+1 fill the other.
   i32x8 fa[2][TN], fb[2][TM];
@@ -522,6 +598,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
     }
   }
 
+  if constexpr (SPLITK)
+    if (!split_k_reduce<TN, TM, NW>(acc, partials, counters, tile, split, splits, wave, lane, &is_last)) return;
   if constexpr (SW) store_tile_sw<BM, BN, WGM, WGN, RANK>(lds, scale_lds, acc, ep, m0, n0, M, N, wm, wn, lane);
   else store_tile<BM, BN, WGM, WGN, RANK>(lds, scale_lds, acc, ep, m0, n0, M, N, wm, wn, lane);
 }
@@ -904,21 +982,45 @@ hipError_t w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64
 // ldw = 0: tiled weights (tiled_w_offset).
 template <int BM, int BN, int WGM, int WGN, int BK, int STAGES>
 static hipError_t launch_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
-                                 const Epilogue& ep, int rank, int group_m, hipStream_t stream) {
+                                 const Epilogue& ep, int rank, int group_m, int splits, float* partials, int* counters,
+                                 hipStream_t stream) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-  const dim3 grid((unsigned)(tm * tn)), block(64 * WGM * WGN);
+  const dim3 grid((unsigned)(tm * tn * splits)), block(64 * WGM * WGN);
   if (group_m < 1) group_m = 1;
 #define JV_PREFILL_LAUNCH(R, PW, PX)                                   \
   gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, R, PW, PX>         \
-      <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep)
+      <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep, splits, partials, counters)
 #define JV_PREFILL_LAUNCH_X(R, PW)             \
   if (ldx == 0) JV_PREFILL_LAUNCH(R, PW, true); \
   else JV_PREFILL_LAUNCH(R, PW, false);
+  if constexpr (BM == 64 && BN == 64) {
+    if (splits > 1) {
+      // split-K: plain or LoRA epilogue (the fused SwiGLU keeps whole k ranges)
+#define JV_PREFILL_LAUNCH_SK(R, PW, PX)                                         \
+  gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, R, PW, PX, false, true>     \
+      <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep, splits, partials, counters)
+#define JV_PREFILL_LAUNCH_SK_X(R, PW)             \
+  if (ldx == 0) JV_PREFILL_LAUNCH_SK(R, PW, true); \
+  else JV_PREFILL_LAUNCH_SK(R, PW, false);
+      if (ep.half) return hipErrorInvalidValue;
+      if (rank == 16) {
+        if (ldw == 0) { JV_PREFILL_LAUNCH_SK_X(16, true) }
+        else { JV_PREFILL_LAUNCH_SK_X(16, false) }
+      } else {
+        if (ldw == 0) { JV_PREFILL_LAUNCH_SK_X(0, true) }
+        else { JV_PREFILL_LAUNCH_SK_X(0, false) }
+      }
+#undef JV_PREFILL_LAUNCH_SK_X
+#undef JV_PREFILL_LAUNCH_SK
+      return hipGetLastError();
+    }
+  }
+  if (splits > 1) return hipErrorInvalidValue;
   if (ep.half) {
     // fused SwiGLU: packed activation codes only
 #define JV_PREFILL_LAUNCH_SW(R, PW)                                      \
   gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, R, PW, true, true>   \
-      <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep)
+      <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep, splits, partials, counters)
     if (rank == 16) {
       if (ldw == 0) JV_PREFILL_LAUNCH_SW(16, true);
       else JV_PREFILL_LAUNCH_SW(16, false);
@@ -976,7 +1078,29 @@ static hipError_t launch_prefill_pp(const uint8_t* xq, int64_t ldx, const uint8_
   return hipGetLastError();
 }
 
-PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count) {
+// K splits for a lockstep tile grid: as many as keep the grid within one
+// round of `per_cu` workgroups per CU (the tile's occupancy), each split
+// keeping at least 4 BK-deep stages, at most kMaxPrefillSplits. A split costs
+// about 3 us (partials written through to the coherent level, the count, the
+// last workgroup's loads), so grids that already give every CU half its
+// workgroups split only for long k ranges (>= 64 stages). Measured on MI355X
+// at M = 65-512 over the 9B shapes (us, one tile per workgroup -> split):
+// down 36.7 -> 21.9 (M = 65, 4 splits), 37.7 -> 33.4 (M = 256, 2); q/o 13.8
+// -> 11.4 (M = 65, 4); k/v 13.3 -> 9.2 (M = 65, 8), 13.3 -> 11.3 (M = 512, 4);
+// but q/o at M = 256 (2 splits) 14.3 -> 15.1, and merged q/k/v at M = 96
+// (192 tiles, 3 splits: past one round) 14.9 -> 17.4.
+static int lockstep_splits(int64_t tiles, int64_t K, int bk, int per_cu, int cu_count) {
+  const int64_t slots = (int64_t)cu_count * per_cu;
+  int64_t s = slots / tiles;
+  if (s < 2) return 1;
+  if (2 * tiles > (int64_t)cu_count && K / bk < 64) return 1;
+  if (s > kMaxPrefillSplits) s = kMaxPrefillSplits;
+  const int64_t most = K / bk / 4;
+  if (s > most) s = most;
+  return s > 1 ? (int)s : 1;
+}
+
+PrefillTile prefill_tile(int64_t M, int64_t N, int64_t K, int cu_count) {
   // 256x256 tiles in the ping-pong form (least L2 -> LDS traffic per flop,
   // and the fastest tile per CU) once they cover five eighths of the CUs,
   // even in a partial round; else the largest lockstep tile that gives every
@@ -998,14 +1122,23 @@ PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count) {
   if (t256x128 == cus || t256x128 >= 2 * cus) return PrefillTile{256, 128, 2, 4, 128, 3, 4};
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
   if (t128 >= 2 * cus) return PrefillTile{128, 128, 2, 2, 128, 4, 8};
-  return PrefillTile{64, 64, 2, 2, 128, 4, 8};
+  // 64x64 tiles, two workgroups per CU; too few of them (short batches on
+  // narrow weights, the regime where the reference splits K below 256 rows,
+  // inference/fp8.py:118-123) split K to fill the CUs.
+  PrefillTile t{64, 64, 2, 2, 128, 4, 8};
+  t.splits = lockstep_splits(((M + 63) / 64) * ((N + 63) / 64), K, t.bk, 2, cu_count);
+  return t;
 }
 
 hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
-                        const Epilogue& ep, int rank, PrefillTile t, hipStream_t stream) {
+                        const Epilogue& ep, int rank, PrefillTile t, float* partials, int* counters,
+                        hipStream_t stream) {
   if (rank != 0 && rank != 16) return hipErrorInvalidValue;
   if (K % t.bk || K % 128) return hipErrorInvalidValue;
   if (ep.half && (ldx != 0 || 2 * ep.half != N || ep.half % 16)) return hipErrorInvalidValue;
+  if (t.splits < 1 || t.splits > kMaxPrefillSplits ||
+      (t.splits > 1 && (t.pingpong || !partials || !counters || K / t.bk < t.splits)))
+    return hipErrorInvalidValue;
   if (t.pingpong) {
     if (t.wgm != 2 || t.wgn != 4 || t.bk != 64) return hipErrorInvalidValue;
 #define JV_PREFILL_PP_CASE(BM_, BN_, ST_) \
@@ -1017,7 +1150,8 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
   }
 #define JV_PREFILL_CASE(BM_, BN_, WGM_, WGN_, BK_, ST_)                                                     \
   if (t.bm == BM_ && t.bn == BN_ && t.wgm == WGM_ && t.wgn == WGN_ && t.bk == BK_ && t.stages == ST_)       \
-    return launch_prefill<BM_, BN_, WGM_, WGN_, BK_, ST_>(xq, ldx, w, ldw, M, N, K, ep, rank, t.group_m, stream);
+    return launch_prefill<BM_, BN_, WGM_, WGN_, BK_, ST_>(xq, ldx, w, ldw, M, N, K, ep, rank, t.group_m, t.splits, partials, \
+                                                         counters, stream);
   // The lockstep shapes prefill_tile picks.
   JV_PREFILL_CASE(256, 128, 2, 4, 128, 3)
   JV_PREFILL_CASE(128, 128, 2, 2, 128, 4)

@@ -50,7 +50,23 @@ struct DecodePlan {
 struct PrefillTile {
   int bm, bn, wgm, wgn, bk, stages, group_m;
   bool pingpong = false;
+  // Lockstep tiles: workgroups per tile, each adding up its own part of the
+  // k range (1: no split).
+  int splits = 1;
 };
+
+// Workspace bytes of a prefill launch with this tile: one fp32 partial tile
+// per (tile, split) when K is split, else 0.
+inline int64_t prefill_partial_bytes(const PrefillTile& t, int64_t M, int64_t N) {
+  if (t.splits < 2) return 0;
+  return ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * t.splits * (int64_t)t.bm * t.bn * 4;
+}
+
+// Tile counters a prefill launch with this tile needs (one per output tile
+// when K is split).
+inline int64_t prefill_counters(const PrefillTile& t, int64_t M, int64_t N) {
+  return t.splits < 2 ? 0 : ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+}
 
 // Byte offset of activation code (m, k) in the packed layout: for token tile
 // mt = m/16 and 128-k step s, two 1 KB halves, each holding 16 bytes per lane
@@ -96,11 +112,14 @@ hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, bool packed_x, const uin
                        const DecodePlan& plan, float* partial, int* counters, const Epilogue& ep, int rank,
                        hipStream_t stream);
 
-PrefillTile prefill_tile(int64_t M, int64_t N, int cu_count);
+PrefillTile prefill_tile(int64_t M, int64_t N, int64_t K, int cu_count);
 // ldx = 0: packed activation codes (packed_x_offset); ldw = 0: tiled weights.
 // ep.half != 0: fused SwiGLU epilogue (packed codes only, N = 2 half).
+// With tile.splits > 1: partials of prefill_partial_bytes and
+// prefill_counters zeroed tile counters (left at zero).
 hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
-                        const Epilogue& ep, int rank, PrefillTile tile, hipStream_t stream);
+                        const Epilogue& ep, int rank, PrefillTile tile, float* partials, int* counters,
+                        hipStream_t stream);
 
 // W8A16 parity mode (bf16 activations x e4m3 weights, the reference's own
 // arithmetic): y = bf16(acc * sw[n]), then bf16(y + bias[n]) with a bias.

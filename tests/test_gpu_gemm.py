@@ -157,6 +157,36 @@ def test_split_k_decode_path(N, K, M):
     assert all(int(c.abs().sum()) == 0 for c in TILE_COUNTERS.values())
 
 
+@pytest.mark.parametrize("N,K,M", [(4096, 4096, 96), (4096, 12288, 128), (1024, 4096, 65), (1024, 4096, 512),
+                                   (128, 4096, 2048), (1040, 2048, 200), (4096, 1024, 100), (4096, 12288, 256)])
+def test_split_k_prefill_path(N, K, M):
+    """Batches past the decode kernel whose 64x64 tiles cannot fill the CUs
+    split K across workgroups (the reference splits K below 256 rows,
+    inference/fp8.py:118-123); the last workgroup of each tile adds the
+    partials in split order: within the GEMM criteria, deterministic, counters
+    left zero, on row-major and tiled weights, with bias and LoRA."""
+    from jeeves_amd import TILE_COUNTERS
+    from jeeves_amd.device import sm_count
+
+    assert _lib.lib().jv_fp8_split_for(M, N, K, sm_count(torch.device("cuda"))) > 1
+    x = synthetic.activations_heavy_tail(M, K, 170 + M).cuda()
+    wq, sw = quantize_rows(synthetic.weight(N, K, 171).cuda())
+    xq, sx = quantize_rows(x)
+    y = fp8_matmul_quantized(xq, sx, wq, sw)
+    check(y, x, wq, sw)
+    assert torch.equal(y, fp8_matmul_quantized(xq, sx, wq, sw)), "split-K result is not deterministic"
+    assert torch.equal(fp8_matmul(x, wq, sw), y)
+    assert torch.equal(fp8_matmul(x, tile_weight(wq), sw, tiled=True), y)
+    a, b = synthetic.lora_factors(N, K, 172)
+    lora = (a.cuda(), b.cuda(), synthetic.LORA_SCALING)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(173)) * 0.1).to(torch.bfloat16).cuda()
+    got = fp8_matmul(x, wq, sw, bias=bias, lora=lora)
+    check(got, x, wq, sw, bias=bias, lora=lora)
+    assert torch.equal(got, (fp8_matmul(x, wq, sw, lora=lora).float() + bias.float()).to(torch.bfloat16))
+    torch.cuda.synchronize()
+    assert all(int(c.abs().sum()) == 0 for c in TILE_COUNTERS.values())
+
+
 @pytest.mark.parametrize("N,K", [(144, 1024), (160, 384), (48, 128), (4112, 256)])
 @pytest.mark.parametrize("M", [1, 5, 16, 40])
 def test_decode_short_k(N, K, M):
