@@ -351,8 +351,10 @@ def test_operands_on_another_device_or_of_the_wrong_size_are_refused():
 
 def test_graph_capture_and_replay():
     """Both kernels under HIP graph capture: replays after new inputs match eager
-    calls (the split-K counters are created outside the capture)."""
-    for M, (N, K) in ((16, (1024, 4096)), (256, (4096, 4096))):
+    calls (the split-K counters are created outside the capture), including
+    the split-K paths of the decode kernel (N = 256) and of the 64x64 prefill
+    tiles (M = 96), whose counters every replay must leave at zero."""
+    for M, (N, K) in ((16, (1024, 4096)), (256, (4096, 4096)), (16, (256, 4096)), (96, (4096, 4096))):
         wq, sw = quantize_rows(synthetic.weight(N, K, 8).cuda())
         static_x = torch.zeros(M, K, dtype=torch.bfloat16, device="cuda")
         fp8_matmul(static_x, wq, sw)  # warm: tile counters exist

@@ -3,7 +3,8 @@ is a library-owned device array per GPU), against jv_fp8_linear with a
 caller-provided workspace and tile counters: bitwise-equal outputs on two
 calls in a row, the second with a smaller input, on the decode kernel with
 split-K (tile counters and partials in the scratch), the decode kernel
-without, the prefill kernels, tiled and row-major weights, bias and LoRA; and
+without, the prefill kernels with and without split-K, tiled and row-major
+weights, bias and LoRA; and
 sizes beyond the scratch are refused with a ValueError-class status before
 any launch."""
 
@@ -52,9 +53,11 @@ def without_workspace(x, w, ldw, sw, bias, lora, N):
 
 
 # (N, K, first M, second M, tiled, bias, lora): split-K decode, plain decode,
-# 64x64 prefill tiles on a wide weight, lockstep and ping-pong prefill tiles.
+# 64x64 prefill tiles on a wide weight, split-K 64x64 prefill tiles (6 and 8
+# splits; 4 and 4), lockstep and ping-pong prefill tiles.
 CASES = [(256, 4096, 16, 5, False, False, False), (4096, 4096, 64, 1, True, True, False),
          (24576, 4096, 48, 17, True, False, False), (1024, 4096, 300, 65, True, True, True),
+         (4096, 12288, 96, 128, False, False, False),
          (24576, 4096, 2048, 256, True, False, True), (4096, 12288, 33, 16, False, True, False)]
 
 
