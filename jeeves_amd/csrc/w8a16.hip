@@ -152,17 +152,20 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
 
   // The workgroup that sees count splits-1 sums every split's partials in
   // split order and resets the counter.
-  // Release: each thread's partial stores are ordered at device scope before
-  // the barrier, and thread 0's acq_rel count after it (the barrier carries
-  // the workgroup's stores to thread 0); the reducing workgroup acquires at
-  // device scope before it reads (inference/fp8.py:94 counts with acq_rel).
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  // Ordering without cache-wide fences: the partials were written with
+  // device-scope atomic stores, which gfx950 performs at the device-coherent
+  // level past each XCD's L2; every thread waits for its stores to complete
+  // (s_waitcnt 0) before the barrier that precedes thread 0's device-scope
+  // count, and the reducing workgroup issues its device-scope loads only after
+  // its own count returned. An agent-scope release/acquire pair instead writes
+  // back and invalidates the whole L2 of the XCD in every finishing
+  // workgroup: 44 vs 6.8 us for two splits at M = 32, N = K = 4096.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
-    is_last = __hip_atomic_fetch_add(counters + group, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+    is_last = __hip_atomic_fetch_add(counters + group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
   __syncthreads();
   if (!is_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int idx = (int)threadIdx.x + j * kThreads;
@@ -170,9 +173,16 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
     const int t = idx >> 8, rt = t / MT, mt = t % MT, e = idx & 255, ml = e >> 4, nl = e & 15;
     const int m = mt * 16 + ml, n = n0 + rt * 16 + nl;
     if (m < M && n < N) {
+      // every split's partial in flight together, then added in split order
+      float part[16];
+#pragma unroll
+      for (int sp = 0; sp < 16; ++sp)
+        if (sp < splits)
+          part[sp] = __hip_atomic_load(partial + ((int64_t)sp * M + m) * N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       float sum = 0.0f;
-      for (int sp = 0; sp < splits; ++sp)
-        sum += __hip_atomic_load(partial + ((int64_t)sp * M + m) * N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int sp = 0; sp < 16; ++sp)
+        if (sp < splits) sum += part[sp];
       y[(int64_t)m * ldy + n] = w8a16_out(sum, pre_sw[j], has_bias, pre_b[j]);
     }
   }
