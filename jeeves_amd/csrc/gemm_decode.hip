@@ -285,13 +285,15 @@ DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count, bool swigl
   // use eight waves in bursts of 4. More token tiles shorten the burst to
   // bound the registers it holds.
   p.waves = K / 128 > 32 ? 8 : 4;
-  // Two or more token tiles on weights of one to two rounds of 16-row tiles
-  // (the merged q/k/v, 6144 x 4096): two tiles per wave and eight waves put
-  // every tile pair in one round (13.8 -> 11.0 us at M = 64, 9.7 -> 8.9 at 32).
-  if (!swiglu && mt >= 2 && tiles > cu_count && tiles <= 2 * (int64_t)cu_count && K / 128 >= 16) {
-    p.rt = 2;
-    p.waves = 8;
-  }
+  // Weights of one to two rounds of 16-row tiles (the merged q/k/v,
+  // 6144 x 4096) take two tiles per wave, so every tile pair runs in one
+  // round: 7.9 -> 7.5 us at 1-16 tokens, 9.7 -> 8.9 at 32, 13.8 -> 11.0 at 64.
+  if (!swiglu && tiles > cu_count && tiles <= 2 * (int64_t)cu_count && K / 128 >= 16) p.rt = 2;
+  // Two tiles per wave stream best as eight waves of four k steps rather than
+  // four waves of eight (gate+up 19.2 -> 18.5 us at M = 1, 20.0 -> 19.7 at
+  // 16), except with the SwiGLU epilogue, whose gate/up pairing keeps four
+  // (quantizer + GEMM 23.1 us with four waves, 24.3 with eight).
+  if (!swiglu && p.rt == 2 && K / 128 >= 16) p.waves = 8;
   p.unroll = decode_unroll((int)mt, p.rt, p.waves);
   const int64_t groups = (tiles + p.rt - 1) / p.rt;
   p.groups = (int)groups;
