@@ -114,7 +114,7 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
 
 /* Bytes of device memory jv_fp8_linear_noalloc keeps per GPU for the rest of
  * the process (its tile counters and workspace). */
-#define JV_FP8_NOALLOC_SCRATCH_BYTES (16 << 20)
+#define JV_FP8_NOALLOC_SCRATCH_BYTES (32 << 20)
 
 /* jv_fp8_linear without a workspace or tile counters, for callers that cannot
  * allocate device memory (code under HIP graph capture that must not touch
@@ -124,9 +124,9 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
  * counters live in a library-owned device array of
  * JV_FP8_NOALLOC_SCRATCH_BYTES per GPU (minus 16 KiB of counters for the
  * workspace: every decode call, M <= 64 and K <= 16384, and on the 9B
- * projection shapes prefill batches up to 4080 tokens at K = 4096 or 1360 at
- * K = 12288 fit; the split-K partials of short batches on narrow weights, up
- * to 8 MiB, share the space, so other shapes can reach the limit sooner).
+ * projection shapes prefill batches up to 8176 tokens at K = 4096 or 2720 at
+ * K = 12288 fit; the split-K partials of the prefill plans, up to 16 MiB,
+ * share the space, so other shapes can reach the limit sooner).
  * Sizes whose jv_fp8_linear_workspace_bytes exceed it return JV_ERR_VALUE. Same results
  * as jv_fp8_linear, bit for bit. Every call on a GPU shares that GPU's
  * scratch: calls that overlap on one GPU (concurrent streams, or host threads

@@ -102,9 +102,8 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, co
                                       stream),
                       "fp8 decode GEMM launch");
   }
-  jv::PrefillTile tile = jv::prefill_tile(M, N, K, cus);
   // The fused SwiGLU GEMM keeps whole k ranges (its callers pass no partials).
-  if (swiglu_half) tile.splits = 1;
+  const jv::PrefillTile tile = jv::prefill_tile(M, N, K, cus, swiglu_half == 0);
   float* partials = nullptr;
   if (tile.splits > 1) {
     const int64_t tiles = jv::prefill_counters(tile, M, N);

@@ -322,6 +322,8 @@ __device__ __forceinline__ void store_tile_sw(uint8_t* lds, const float* scale_l
 // so they read completed partials. No cache-wide writeback or invalidation
 // (an agent-scope release/acquire pair) is needed on this path.
 constexpr int kMaxPrefillSplits = 8;
+// Largest split-K partial workspace a prefill plan uses.
+constexpr int64_t kMaxPrefillPartialBytes = 16 << 20;
 
 template <int TN, int TM, int NW>
 __device__ __forceinline__ bool split_k_reduce(f32x16 (&acc)[TN][TM], float* __restrict__ partials,
@@ -993,7 +995,7 @@ static hipError_t launch_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* 
 #define JV_PREFILL_LAUNCH_X(R, PW)             \
   if (ldx == 0) JV_PREFILL_LAUNCH(R, PW, true); \
   else JV_PREFILL_LAUNCH(R, PW, false);
-  if constexpr (BM == 64 && BN == 64) {
+  {
     if (splits > 1) {
       // split-K: plain or LoRA epilogue (the fused SwiGLU keeps whole k ranges)
 #define JV_PREFILL_LAUNCH_SK(R, PW, PX)                                         \
@@ -1078,56 +1080,71 @@ static hipError_t launch_prefill_pp(const uint8_t* xq, int64_t ldx, const uint8_
   return hipGetLastError();
 }
 
-// K splits for a lockstep tile grid: as many as keep the grid within one
-// round of `per_cu` workgroups per CU (the tile's occupancy), each split
-// keeping at least 4 BK-deep stages, at most kMaxPrefillSplits. A split costs
-// about 3 us (partials written through to the coherent level, the count, the
-// last workgroup's loads), so grids that already give every CU half its
-// workgroups split only for long k ranges (>= 64 stages). Measured on MI355X
-// at M = 65-512 over the 9B shapes (us, one tile per workgroup -> split):
-// down 36.7 -> 21.9 (M = 65, 4 splits), 37.7 -> 33.4 (M = 256, 2); q/o 13.8
-// -> 11.4 (M = 65, 4); k/v 13.3 -> 9.2 (M = 65, 8), 13.3 -> 11.3 (M = 512, 4);
-// but q/o at M = 256 (2 splits) 14.3 -> 15.1, and merged q/k/v at M = 96
-// (192 tiles, 3 splits: past one round) 14.9 -> 17.4.
-static int lockstep_splits(int64_t tiles, int64_t K, int bk, int per_cu, int cu_count) {
-  const int64_t slots = (int64_t)cu_count * per_cu;
-  int64_t s = slots / tiles;
-  if (s < 2) return 1;
-  if (2 * tiles > (int64_t)cu_count && K / bk < 64) return 1;
-  if (s > kMaxPrefillSplits) s = kMaxPrefillSplits;
-  const int64_t most = K / bk / 4;
-  if (s > most) s = most;
-  return s > 1 ? (int)s : 1;
+// Time model of a lockstep launch, fitted (least squares on log time) to
+// 423 timings on MI355X of the three lockstep tiles at 1-8 K splits over the
+// 9B projection shapes (q/o, k/v, merged q/k/v, gate+up, down) at M = 65-1536.
+// Workgroups run in rounds of cu_count * per_cu. Per 4096 of K a workgroup
+// takes `light` us in a round with few workgroups and `full` us in a full one
+// (HBM, L2 and LDS bandwidth shared), plus `item` us of prologue and
+// epilogue; a split launch adds the partial write, the count and the last
+// workgroup's loads, growing with the partial tile bytes and the rounds. The
+// argmin of the model is within 1.5% of the fastest measured choice summed
+// over those shapes (the fixed tile rules it replaces: 20%).
+struct LockstepCost {
+  PrefillTile tile;
+  int per_cu;         // workgroups per CU (LDS and VGPR occupancy)
+  double light, full, item;
+};
+static const LockstepCost kLockstepCosts[] = {
+    {{256, 128, 2, 4, 128, 3, 4}, 1, 27.28, 37.26, 5.03},
+    {{128, 128, 2, 2, 128, 4, 8}, 1, 16.30, 19.58, 4.48},
+    {{64, 64, 2, 2, 128, 4, 8}, 2, 10.48, 16.23, 1.08},
+};
+// A split launch: a fixed cost, a cost per split, and a cost per split of a
+// 128x128 fp32 partial per round.
+constexpr double kSplitBaseUs = 3.63, kSplitEachUs = 0.49, kSplitPerTileUs = 0.40;
+
+static double lockstep_time_us(const LockstepCost& c, int64_t M, int64_t N, int64_t K, int splits, int cu_count) {
+  const int64_t tiles = ((M + c.tile.bm - 1) / c.tile.bm) * ((N + c.tile.bn - 1) / c.tile.bn);
+  const int64_t items = tiles * splits, slots = (int64_t)cu_count * c.per_cu;
+  const int64_t rounds = items / slots, rest = items % slots;
+  const double k = (double)K / 4096.0 / splits;
+  double t = rounds * (c.full * k + c.item);
+  if (rest) t += (c.light + (c.full - c.light) * (double)rest / slots) * k + c.item;
+  if (splits > 1) {
+    const double round_count = items > slots ? (double)items / slots : 1.0;
+    t += kSplitBaseUs + kSplitEachUs * splits + kSplitPerTileUs * splits * (c.tile.bm * c.tile.bn / 16384.0) * round_count;
+  }
+  return t;
 }
 
-PrefillTile prefill_tile(int64_t M, int64_t N, int64_t K, int cu_count) {
-  // 256x256 tiles in the ping-pong form (least L2 -> LDS traffic per flop,
-  // and the fastest tile per CU) once they cover five eighths of the CUs,
-  // even in a partial round; else the largest lockstep tile that gives every
-  // CU whole rounds of work: 256x128 at one per CU or two or more, 128x128 at
-  // two or more, else 64x64, whose 64 KB of LDS lets two workgroups share a CU
-  // (one's prologue and epilogue overlap the other's main loop). Measured on
-  // MI355X over the 9B projection shapes at M = 512, 2048 and 8192: gate+up
-  // at M = 512 (192 tiles of 256x256) 52.7 us against 72 us with 128x128 and
-  // 74 us with 256x128; k/v at M = 2048 21.9 -> 15.3 us with 64x64 instead of
-  // 128x128; q/o at M = 2048 (128 tiles of 256x256) keep 256x128 (39 vs 49 us).
+PrefillTile prefill_tile(int64_t M, int64_t N, int64_t K, int cu_count, bool split_k) {
   // Batches of at most 64 tokens that reach the prefill kernel (wide weights,
   // decode_kernel_for) take 64x64 tiles: 23.4 us for gate+up at M = 64 vs
   // 25.9 with 64x128 and 45.9 with 128x64.
   if (M <= kDecodeMaxRows) return {64, 64, 2, 2, 128, 4, 8};
+  // 256x256 tiles in the ping-pong form (least L2 -> LDS traffic per flop,
+  // and the fastest tile per CU) once they cover five eighths of the CUs,
+  // even in a partial round: gate+up at M = 512 (192 tiles) 52.7 us against
+  // 72 us with 128x128 and 74 us with 256x128.
   const int64_t cus = cu_count;
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
   if (t256 * 8 >= cus * 5) return PrefillTile{256, 256, 2, 4, 64, 4, 4, true};
-  const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
-  if (t256x128 == cus || t256x128 >= 2 * cus) return PrefillTile{256, 128, 2, 4, 128, 3, 4};
-  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-  if (t128 >= 2 * cus) return PrefillTile{128, 128, 2, 2, 128, 4, 8};
-  // 64x64 tiles, two workgroups per CU; too few of them (short batches on
-  // narrow weights, the regime where the reference splits K below 256 rows,
-  // inference/fp8.py:118-123) split K to fill the CUs.
-  PrefillTile t{64, 64, 2, 2, 128, 4, 8};
-  t.splits = lockstep_splits(((M + 63) / 64) * ((N + 63) / 64), K, t.bk, 2, cu_count);
-  return t;
+  // Else the lockstep tile and K split of least modelled time; each split
+  // keeps at least four BK-deep stages and the partials at most
+  // kMaxPrefillPartialBytes.
+  PrefillTile best{64, 64, 2, 2, 128, 4, 8};
+  double best_us = 1e300;
+  for (const LockstepCost& c : kLockstepCosts) {
+    for (int s = 1; s <= (split_k ? kMaxPrefillSplits : 1); ++s) {
+      PrefillTile t = c.tile;
+      t.splits = s;
+      if (s > 1 && (K / t.bk < 4 * s || prefill_partial_bytes(t, M, N) > kMaxPrefillPartialBytes)) break;
+      const double us = lockstep_time_us(c, M, N, K, s, cu_count);
+      if (us < best_us) best_us = us, best = t;
+    }
+  }
+  return best;
 }
 
 hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,

@@ -112,7 +112,8 @@ hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, bool packed_x, const uin
                        const DecodePlan& plan, float* partial, int* counters, const Epilogue& ep, int rank,
                        hipStream_t stream);
 
-PrefillTile prefill_tile(int64_t M, int64_t N, int64_t K, int cu_count);
+// split_k = false: plans without K splits only (the fused SwiGLU epilogue).
+PrefillTile prefill_tile(int64_t M, int64_t N, int64_t K, int cu_count, bool split_k = true);
 // ldx = 0: packed activation codes (packed_x_offset); ldw = 0: tiled weights.
 // ep.half != 0: fused SwiGLU epilogue (packed codes only, N = 2 half).
 // With tile.splits > 1: partials of prefill_partial_bytes and

@@ -84,22 +84,24 @@ def test_split_for_is_pure_host_logic(product_lib):
     assert L.jv_fp8_split_for(16, 128, 12288, 256) == 12  # 8 tiles; K=12288 runs 8 waves: capped at K/128/8
     assert L.jv_fp8_counters_needed(16, 256, 4096, 256) == 16
     assert L.jv_fp8_counters_needed(16, 4096, 4096, 256) == 0
-    # prefill: the 64x64 tiles split K as far as one round of two workgroups
-    # per CU allows, keeping at least four 128-deep stages per split, at most 8;
-    # grids that already give every CU one workgroup split only long k ranges
-    assert L.jv_fp8_split_for(96, 4096, 4096, 256) == 4     # 128 tiles
+    # prefill: the lockstep tile and K split of least modelled time; a split
+    # keeps at least four 128-deep stages, at most 8
+    assert L.jv_fp8_split_for(96, 4096, 4096, 256) == 4     # 128 tiles of 64x64
     assert L.jv_fp8_counters_needed(96, 4096, 4096, 256) == 128
     assert L.jv_fp8_split_for(96, 4096, 12288, 256) == 4
-    assert L.jv_fp8_split_for(96, 6144, 4096, 256) == 1     # 192 tiles, K = 4096
-    assert L.jv_fp8_split_for(256, 4096, 12288, 256) == 2   # 256 tiles, K = 12288
-    assert L.jv_fp8_split_for(256, 4096, 4096, 256) == 1
-    assert L.jv_fp8_split_for(128, 1024, 4096, 256) == 8    # 32 tiles
+    assert L.jv_fp8_split_for(96, 6144, 4096, 256) == 2     # 192 tiles
+    assert L.jv_fp8_split_for(256, 4096, 12288, 256) == 4   # 64 tiles of 128x128
+    assert L.jv_fp8_counters_needed(256, 4096, 12288, 256) == 64
+    assert L.jv_fp8_split_for(512, 4096, 12288, 256) == 2   # 128 tiles of 128x128
+    assert L.jv_fp8_split_for(128, 1024, 4096, 256) == 4    # 32 tiles
     assert L.jv_fp8_split_for(256, 1024, 512, 256) == 1     # 4 stages of 128 leave no room to split
     assert L.jv_fp8_split_for(512, 1024, 4096, 256) == 4    # 128 tiles
-    assert L.jv_fp8_split_for(2048, 128, 4096, 256) == 8    # 64 tiles
     assert L.jv_fp8_split_for(512, 4096, 4096, 256) == 1    # 512 tiles fill the CUs
+    assert L.jv_fp8_split_for(1040, 2048, 4096, 256) == 1
     assert L.jv_fp8_split_for(2048, 4096, 4096, 256) == 1   # 256x128 tiles
     assert L.jv_fp8_counters_needed(2048, 4096, 4096, 256) == 0
+    assert L.jv_fp8_split_for(65, 24576, 4096, 256) == 1    # 192 tiles of 128x128
+    assert L.jv_fp8_split_for(4096, 24576, 4096, 256) == 1  # 256x256 ping-pong tiles never split
 
 
 def test_wide_weights_never_split_k(product_lib):

@@ -158,10 +158,12 @@ def test_split_k_decode_path(N, K, M):
 
 
 @pytest.mark.parametrize("N,K,M", [(4096, 4096, 96), (4096, 12288, 128), (1024, 4096, 65), (1024, 4096, 512),
-                                   (128, 4096, 2048), (1040, 2048, 200), (4096, 1024, 100), (4096, 12288, 256)])
+                                   (128, 4096, 2048), (1040, 4096, 200), (4096, 12288, 256), (4096, 12288, 512),
+                                   (4112, 12288, 300), (2064, 12288, 333)])
 def test_split_k_prefill_path(N, K, M):
-    """Batches past the decode kernel whose 64x64 tiles cannot fill the CUs
-    split K across workgroups (the reference splits K below 256 rows,
+    """Batches past the decode kernel whose lockstep tiles cannot fill the
+    CUs (64x64 tiles; 128x128 tiles on long k ranges, 2-5 splits, ragged M
+    and N) split K across workgroups (the reference splits K below 256 rows,
     inference/fp8.py:118-123); the last workgroup of each tile adds the
     partials in split order: within the GEMM criteria, deterministic, counters
     left zero, on row-major and tiled weights, with bias and LoRA."""

@@ -53,11 +53,12 @@ def without_workspace(x, w, ldw, sw, bias, lora, N):
 
 
 # (N, K, first M, second M, tiled, bias, lora): split-K decode, plain decode,
-# 64x64 prefill tiles on a wide weight, split-K 64x64 prefill tiles (6 and 8
-# splits; 4 and 4), lockstep and ping-pong prefill tiles.
+# 64x64 prefill tiles on a wide weight, split-K 64x64 prefill tiles (4
+# splits), split-K 128x128 prefill tiles (2 and 4 splits, 16 MiB of
+# partials), lockstep and ping-pong prefill tiles.
 CASES = [(256, 4096, 16, 5, False, False, False), (4096, 4096, 64, 1, True, True, False),
          (24576, 4096, 48, 17, True, False, False), (1024, 4096, 300, 65, True, True, True),
-         (4096, 12288, 96, 128, False, False, False),
+         (4096, 12288, 96, 128, False, False, False), (4096, 12288, 512, 256, True, False, True),
          (24576, 4096, 2048, 256, True, False, True), (4096, 12288, 33, 16, False, True, False)]
 
 
@@ -83,11 +84,11 @@ def test_noalloc_equals_workspace_entry(N, K, M1, M2, tiled, use_bias, use_lora)
 
 def test_noalloc_refuses_sizes_beyond_its_scratch():
     L = _lib.lib()
-    limit = 16 << 20
-    for M, K in ((4096, 4096), (1376, 12288), (8192, 4096)):
+    limit = 32 << 20
+    for M, K in ((8192, 4096), (2736, 12288), (16384, 4096)):
         assert L.jv_fp8_linear_workspace_bytes(M, 4096, K, 0) > limit - 16384
         rc = L.jv_fp8_linear_noalloc(16, K, 16, 0, 16, None, None, None, 0, 0.0, 16, 4096, M, 4096, K,
                                      torch.cuda.current_stream().cuda_stream)
         assert rc == _lib.JV_ERR_VALUE and b"needs" in L.jv_fp8_last_error(), (M, K)
-    assert L.jv_fp8_linear_workspace_bytes(4080, 4096, 4096, 0) <= limit - 16384
-    assert L.jv_fp8_linear_workspace_bytes(1360, 4096, 12288, 0) <= limit - 16384
+    assert L.jv_fp8_linear_workspace_bytes(8176, 4096, 4096, 0) <= limit - 16384
+    assert L.jv_fp8_linear_workspace_bytes(2720, 4096, 12288, 0) <= limit - 16384
