@@ -43,24 +43,50 @@ def compile_device(source: Path, out_dir: Path) -> tuple[str, str]:
     return r.stderr, asm.read_text()
 
 
+BRANCH = re.compile(r"^\s*(s_cbranch_\w+|s_branch)\s+(\S+)")
+LABEL = re.compile(r"^(\.L\w+):")
+
+
 def unguarded_mfmas(asm: str) -> dict[str, list[int]]:
-    """Functions with an MFMA after an EXEC-narrowing instruction and before
-    both the matching restore and any s_cbranch_execz (a linear scan of the
-    listing: per function, the lines of each such MFMA)."""
+    """Functions with an MFMA reached with EXEC narrowed by a divergent guard
+    and neither restored nor checked by an s_cbranch_execz since: a scan of
+    the listing that follows the branches (a branch taken in that state
+    carries it to its label; an unconditional branch ends the fall-through),
+    repeated until the labels' states settle. Per function, the lines of each
+    such MFMA."""
     bad: dict[str, list[int]] = {}
-    fn, narrowed, guarded = None, False, False
-    for no, line in enumerate(asm.splitlines(), 1):
-        m = FUNCTION_LABEL.match(line)
-        if m and not m.group(1).startswith(".L"):
-            fn, narrowed, guarded = m.group(1), False, False
-        elif EXEC_RESTORE.match(line):
-            narrowed = guarded = False
-        elif EXEC_NARROW.match(line):
-            narrowed, guarded = True, False
-        elif re.match(r"^\s*s_cbranch_execz", line):
-            guarded = True
-        elif narrowed and not guarded and re.match(r"^\s*v_mfma", line):
-            bad.setdefault(fn, []).append(no)
+    lines = asm.splitlines()
+    starts = [i for i, line in enumerate(lines) if (m := FUNCTION_LABEL.match(line)) and not m.group(1).startswith(".L")]
+    for s, e in zip(starts, starts[1:] + [len(lines)]):
+        fn = FUNCTION_LABEL.match(lines[s]).group(1)
+        entered: set[str] = set()  # labels some branch reaches with EXEC narrowed and unchecked
+        while True:
+            before = len(entered)
+            found, state, falls = [], False, True
+            for no in range(s + 1, e):
+                line = lines[no]
+                if m := LABEL.match(line):
+                    state = (state and falls) or m.group(1) in entered
+                    falls = True
+                elif EXEC_RESTORE.match(line):
+                    state = False
+                elif EXEC_NARROW.match(line):
+                    state = True
+                elif re.match(r"^\s*s_cbranch_execz", line):
+                    state = False
+                elif m := BRANCH.match(line):
+                    if state:
+                        entered.add(m.group(2))
+                    if m.group(1) == "s_branch":
+                        state, falls = False, False
+                elif re.match(r"^\s*(s_endpgm|s_setpc_b64)", line):
+                    state, falls = False, False
+                elif state and re.match(r"^\s*v_mfma", line):
+                    found.append(no + 1)
+            if len(entered) == before:
+                break
+        if found:
+            bad[fn] = found
     return bad
 
 
@@ -107,3 +133,19 @@ ok:
 \tv_mfma_f32_16x16x128_f8f6f4 v[50:53], v[2:9], v[26:33], v[50:53]
 """
     assert unguarded_mfmas(listing) == {"kern": [3]}
+    # A narrowed block that branches away: the block laid out after it is
+    # not reached in that state, the branch target is.
+    listing = """kern:
+\ts_and_saveexec_b64 s[4:5], s[16:17]
+\ts_cbranch_scc1 .LBB0_9
+\ts_branch .LBB0_8
+.LBB0_7:
+\tv_mfma_f32_16x16x128_f8f6f4 v[66:69], v[2:9], v[34:41], 0
+.LBB0_8:
+\ts_or_b64 exec, exec, s[4:5]
+\ts_endpgm
+.LBB0_9:
+\tv_mfma_f32_16x16x128_f8f6f4 v[66:69], v[2:9], v[34:41], 0
+\ts_branch .LBB0_7
+"""
+    assert unguarded_mfmas(listing) == {"kern": [6, 11]}
