@@ -424,7 +424,8 @@ def quantize_swiglu_output(h: torch.Tensor, amax: torch.Tensor | None = None, *,
     ``(codes, scales)``, plus ``t = h A^T`` (float32 [M,r]) with ``lora_a``.
     ``packed``: codes as a flat uint8 buffer in the GEMMs' fragment order (for
     ``fp8_matmul_quantized(..., packed_rows=M)``); ``amax``: the maxima
-    ``gate_up_swiglu(..., amax=True)`` returned with h."""
+    ``gate_up_swiglu(..., amax=True)`` returned with h, accepted but not read
+    (each row's maximum comes from h in the same pass that encodes it)."""
     M, I = h.shape
     dev = h.device
     if dev.type != "cuda" or h.dtype != torch.bfloat16:
