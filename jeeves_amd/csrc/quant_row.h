@@ -81,25 +81,31 @@ __device__ __forceinline__ void quant_row(int row, const uint16_t* __restrict__ 
 #pragma unroll
   for (int r = 0; r < (RANK > 0 ? RANK : 1); ++r) t[r] = 0.0f;
 
+  // Every chunk's loads are issued before any is used (the index clamped to
+  // the row, so they are unconditional): loads guarded one by one would each
+  // wait for the previous chunk's data.
+  uint4 u[SWIGLU ? NC : 1];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int64_t c = min(tid + i * THREADS, nchunks - 1);
+    v[i] = *reinterpret_cast<const uint4*>(xr + c * 8);
+    if constexpr (SWIGLU) u[i] = *reinterpret_cast<const uint4*>(up + (int64_t)row * ldu + c * 8);
+  }
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int c = tid + i * THREADS;
+    if constexpr (SWIGLU)
+      v[i] = uint4{swiglu_pair(v[i].x, u[i].x), swiglu_pair(v[i].y, u[i].y), swiglu_pair(v[i].z, u[i].z),
+                   swiglu_pair(v[i].w, u[i].w)};
     if (c < nchunks) {
-      if constexpr (SWIGLU) {
-        const uint4 g = *reinterpret_cast<const uint4*>(xr + (int64_t)c * 8);
-        const uint4 u = *reinterpret_cast<const uint4*>(up + (int64_t)row * ldu + (int64_t)c * 8);
-        v[i] = uint4{swiglu_pair(g.x, u.x), swiglu_pair(g.y, u.y), swiglu_pair(g.z, u.z), swiglu_pair(g.w, u.w)};
-        if (h_out) *reinterpret_cast<uint4*>(h_out + (int64_t)row * ldh + (int64_t)c * 8) = v[i];
-      } else {
-        v[i] = *reinterpret_cast<const uint4*>(xr + (int64_t)c * 8);
-      }
-      am = pk_max_u16(am, v[i].x & 0x7FFF7FFFu);
-      am = pk_max_u16(am, v[i].y & 0x7FFF7FFFu);
-      am = pk_max_u16(am, v[i].z & 0x7FFF7FFFu);
-      am = pk_max_u16(am, v[i].w & 0x7FFF7FFFu);
+      if (SWIGLU && h_out) *reinterpret_cast<uint4*>(h_out + (int64_t)row * ldh + (int64_t)c * 8) = v[i];
     } else {
       v[i] = uint4{0, 0, 0, 0};
     }
+    am = pk_max_u16(am, v[i].x & 0x7FFF7FFFu);
+    am = pk_max_u16(am, v[i].y & 0x7FFF7FFFu);
+    am = pk_max_u16(am, v[i].z & 0x7FFF7FFFu);
+    am = pk_max_u16(am, v[i].w & 0x7FFF7FFFu);
   }
   if constexpr (RANK > 0) {
     // A's chunks are loaded 8 ranks at a time, the next batch while this
