@@ -902,6 +902,24 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_prefill_kernel(
   // register r, channel 8*(r/4) + 4*(l/32) + r%4.
   lds_barrier();
   const bool has_bias = bias != nullptr;
+  // The thread's channel scales and biases, every load issued before any is
+  // used (loaded next to their use, each waited for the one before it).
+  float swv[TN][4][4], bv[TN][4][4];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) swv[j][qd][e] = sw[min(n0 + wn * WN + j * 32 + 8 * qd + 4 * (lane >> 5) + e, N - 1)];
+  if (has_bias) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          bv[j][qd][e] = bf16_to_f32(bias[min(n0 + wn * WN + j * 32 + 8 * qd + 4 * (lane >> 5) + e, N - 1)]);
+  }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -910,9 +928,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_prefill_kernel(
       uint32_t hv[TM][4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int n = min(n0 + nl + e, N - 1);
-        const float swn = sw[n];
-        const float bn = has_bias ? bf16_to_f32(bias[n]) : 0.0f;
+        const float swn = swv[j][qd][e];
+        const float bn = has_bias ? bv[j][qd][e] : 0.0f;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
           uint32_t v = f32_to_bf16(acc[j][i][4 * qd + e] * swn);
