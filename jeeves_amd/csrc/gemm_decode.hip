@@ -338,12 +338,6 @@ static void launch_decode_rt(const uint8_t* xq, int64_t ldxq, const uint8_t* w, 
   if constexpr (SW) {
     launch_decode_wu<MT, 2, PACKX, RANK, true>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
   } else {
-    if constexpr (MT >= 2) {
-      if (p.rt == 4) {
-        launch_decode_wu<MT, 4, PACKX, RANK, false>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
-        return;
-      }
-    }
     if (p.rt == 2)
       launch_decode_wu<MT, 2, PACKX, RANK, false>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
     else
@@ -368,7 +362,7 @@ static hipError_t launch_decode_mt(const uint8_t* xq, int64_t ldxq, const uint8_
 hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, bool packed_x, const uint8_t* w, int64_t ldw, int M, int N, int K,
                        const DecodePlan& plan, float* partial, int* counters, const Epilogue& ep, int rank,
                        hipStream_t stream) {
-  if (M < 1 || M > kDecodeMaxRows || (rank != 0 && rank != 16)) return hipErrorInvalidValue;
+  if (M < 1 || M > kDecodeMaxRows || (rank != 0 && rank != 16) || (plan.rt != 1 && plan.rt != 2)) return hipErrorInvalidValue;
   if (ep.half) {
     // Fused SwiGLU: packed activation codes only (jv_fp8_linear_swiglu packs them), one gate/up pair per wave.
     if (!packed_x || plan.rt != 2 || plan.splits != 1 || 2 * ep.half != N || ep.half % 16) return hipErrorInvalidValue;

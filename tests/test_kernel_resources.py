@@ -8,6 +8,10 @@
   registers hold. (A decode kernel whose k bounds lived in vector registers
   had exactly this: the guarded third step of a two-step tail burst added
   address bits to the sums.)
+* no kernel serializes its global loads: a load followed at once by a wait
+  for every outstanding load, repeated, is what a load guarded one at a time
+  next to its use compiles to (the quantizer's per-chunk loads were, one
+  memory round trip per chunk).
 """
 
 from __future__ import annotations
@@ -149,3 +153,42 @@ ok:
 \ts_branch .LBB0_7
 """
     assert unguarded_mfmas(listing) == {"kern": [6, 11]}
+
+
+def serialized_loads(asm: str) -> dict[str, int]:
+    """Per function, the global loads (not global -> LDS copies) whose next
+    instruction waits for every outstanding vector-memory operation."""
+    counts: dict[str, int] = {}
+    fn = None
+    lines = [line.strip() for line in asm.splitlines()]
+    for no, line in enumerate(lines):
+        if (m := FUNCTION_LABEL.match(line)) and not m.group(1).startswith(".L"):
+            fn = m.group(1)
+        elif line.startswith("global_load") and not line.startswith("global_load_lds"):
+            nxt = next((u for u in lines[no + 1:no + 4] if u and not u.startswith(";")), "")
+            if nxt.startswith("s_waitcnt") and "vmcnt(0)" in nxt:
+                counts[fn] = counts.get(fn, 0) + 1
+    return counts
+
+
+def test_no_kernel_serializes_its_loads(device_builds):
+    bad = {}
+    for src, (_, asm) in device_builds.items():
+        for fn, n in serialized_loads(asm).items():
+            if n >= 3:
+                bad[f"{src}:{fn[:80]}"] = n
+    assert not bad, bad
+
+
+def test_scan_finds_serialized_loads():
+    listing = """kern:
+\tglobal_load_dwordx4 v[2:5], v1, s[2:3]
+\ts_waitcnt vmcnt(0)
+\tv_pk_max_u16 v1, v1, v2
+\tglobal_load_dwordx4 v[6:9], v1, s[2:3]
+\tglobal_load_dwordx4 v[10:13], v1, s[2:3]
+\ts_waitcnt vmcnt(1)
+\tglobal_load_lds_dwordx4 v[2:3], off
+\ts_waitcnt vmcnt(0)
+"""
+    assert serialized_loads(listing) == {"kern": 1}
