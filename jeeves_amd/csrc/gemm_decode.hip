@@ -36,12 +36,17 @@ constexpr int kMaxDecodeSplits = 16;
 
 // SW: fused SwiGLU (gate+up weights, Epilogue::half): the wave's tiles come in
 // (gate p, up p) pairs, and the epilogue stores h (no split-K).
-template <int MT, int RT, int WAVES, int UNROLL, bool PACKX, int RANK, bool PACKW, bool SW = false>
+// SPLIT: workgroups split K (grid.y = splits > 1). Without it each wave's k
+// range is its share of the whole row with the compile-time divisor WAVES;
+// with the split count a run-time value the same kernel took 1 us longer
+// at M = 16 on gate+up (19.7 vs 18.7 us), even at one split.
+template <int MT, int RT, int WAVES, int UNROLL, bool PACKX, int RANK, bool PACKW, bool SW = false, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* __restrict__ xq, int64_t ldxq,
                                                                  const uint8_t* __restrict__ w, int64_t ldw, int M, int N,
                                                                  int K, int splits, float* __restrict__ partial,
                                                                  int* __restrict__ counters, Epilogue ep) {
   static_assert(!SW || RT % 2 == 0, "SwiGLU pairs each gate tile with its up tile");
+  static_assert(!(SW && SPLIT), "the SwiGLU epilogue keeps whole k ranges");
   __shared__ f32x4 red[WAVES][RT * MT][64];
   __shared__ int is_last;
   const int lane = threadIdx.x & 63;
@@ -53,14 +58,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   // scan in the kernel-resource tests).
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int group = blockIdx.x;
-  const int split = blockIdx.y;
+  const int split = SPLIT ? (int)blockIdx.y : 0;
   const int n0 = group * 16 * RT;
 
   const int ksteps = K >> 7;
-  const int slices = splits * WAVES;
-  const int slice = split * WAVES + wave;
-  const int s_begin = (int)((int64_t)ksteps * slice / slices);
-  const int s_end = (int)((int64_t)ksteps * (slice + 1) / slices);
+  int s_begin, s_end;
+  if constexpr (SPLIT) {
+    const int slice = split * WAVES + wave;
+    s_begin = slice_begin<WAVES>(ksteps, slice, splits);
+    s_end = slice_begin<WAVES>(ksteps, slice + 1, splits);
+  } else {
+    s_begin = ksteps * wave / WAVES;
+    s_end = ksteps * (wave + 1) / WAVES;
+  }
 
   const int li = lane & 15;
   const int lk = (lane >> 4) * 32;
@@ -123,25 +133,32 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
   // MFMAs consume them. A full burst is straight-line code, so each step's
   // MFMAs wait only for that step's data; the last, partial burst guards each
   // step with a scalar branch (s and s_end are wave-uniform).
+  // The burst's addresses are one base per operand plus constant offsets
+  // (u steps of 2 KB packed or 128 B row-major), which the loads take as
+  // immediates instead of a 64-bit add per step (0.5 us of the 1 us above).
   auto burst = [&](int s, auto full) {
     constexpr bool FULL = decltype(full)::value;
+    constexpr int WSTEP = PACKW ? 2048 : 128, XSTEP = PACKX ? 2048 : 128;
     i32x4 wa[UNROLL][RT][2];
     i32x4 xa[UNROLL][MT][2];
+    const uint8_t* wb[RT];
+    const uint8_t* xb[MT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) wb[rt] = wp[rt] + (int64_t)s * WSTEP;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xb[mt] = xp[mt] + (int64_t)s * XSTEP;
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       if (!FULL && s + u >= s_end) break;
-      const int64_t off = (int64_t)(s + u) * 128;
-      const int64_t woff = PACKW ? (int64_t)(s + u) * 2048 : off;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        wa[u][rt][0] = *reinterpret_cast<const i32x4*>(wp[rt] + woff);
-        wa[u][rt][1] = *reinterpret_cast<const i32x4*>(wp[rt] + woff + (PACKW ? 1024 : 16));
+        wa[u][rt][0] = *reinterpret_cast<const i32x4*>(wb[rt] + u * WSTEP);
+        wa[u][rt][1] = *reinterpret_cast<const i32x4*>(wb[rt] + u * WSTEP + (PACKW ? 1024 : 16));
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int64_t xo = PACKX ? (int64_t)(s + u) * 2048 : off;
-        xa[u][mt][0] = *reinterpret_cast<const i32x4*>(xp[mt] + xo);
-        xa[u][mt][1] = *reinterpret_cast<const i32x4*>(xp[mt] + xo + (PACKX ? 1024 : 16));
+        xa[u][mt][0] = *reinterpret_cast<const i32x4*>(xb[mt] + u * XSTEP);
+        xa[u][mt][1] = *reinterpret_cast<const i32x4*>(xb[mt] + u * XSTEP + (PACKX ? 1024 : 16));
       }
     }
     if constexpr (FULL) __builtin_amdgcn_sched_barrier(0);
@@ -221,13 +238,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
     for (int wv = 0; wv < WAVES; ++wv) sum += redf[wv * RT * MT * 256 + src];
     const int m = mt * 16 + ml, n = n0 + rt * 16 + nl;
     if (m < M && n < N) {
-      if (splits == 1)
+      if (!SPLIT || splits == 1)
         ep.y[(int64_t)m * ep.ldy + n] =
             (uint16_t)f32_to_bf16(epilogue_value<RANK>(ep, sum, m, n, pre_sx[j], pre_sw[j], pre_b[j]));
       else  // device-coherent store: visible to the reducing workgroup without a cache flush
         __hip_atomic_store(partial + ((int64_t)split * M + m) * N + n, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  if constexpr (!SPLIT) return;
   if (splits == 1) return;
 
   // The workgroup that sees count splits-1 sums every split's partials in
@@ -310,16 +328,32 @@ DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count, bool swigl
   return p;
 }
 
+template <int MT, int RT, int W, int U, bool PACKX, int RANK, bool SW, bool SPLIT>
+static void launch_decode_split(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                                const DecodePlan& p, float* partial, int* counters, const Epilogue& ep,
+                                hipStream_t stream) {
+  const dim3 grid((unsigned)p.groups, (unsigned)p.splits), block(64 * W);
+  if (ldw == 0)
+    gemm_decode_kernel<MT, RT, W, U, PACKX, RANK, true, SW, SPLIT>
+        <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, p.splits, partial, counters, ep);
+  else
+    gemm_decode_kernel<MT, RT, W, U, PACKX, RANK, false, SW, SPLIT>
+        <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, p.splits, partial, counters, ep);
+}
+
+// K splits come only with one tile per wave (decode_plan splits narrow
+// weights, whose tiles take one wave each), so only those shapes have
+// split instances.
 template <int MT, int RT, int W, int U, bool PACKX, int RANK, bool SW>
 static void launch_decode(const uint8_t* xq, int64_t ldxq, const uint8_t* w, int64_t ldw, int M, int N, int K,
                           const DecodePlan& p, float* partial, int* counters, const Epilogue& ep, hipStream_t stream) {
-  const dim3 grid((unsigned)p.groups, (unsigned)p.splits), block(64 * W);
-  if (ldw == 0)
-    gemm_decode_kernel<MT, RT, W, U, PACKX, RANK, true, SW>
-        <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, p.splits, partial, counters, ep);
-  else
-    gemm_decode_kernel<MT, RT, W, U, PACKX, RANK, false, SW>
-        <<<grid, block, 0, stream>>>(xq, ldxq, w, ldw, M, N, K, p.splits, partial, counters, ep);
+  if constexpr (RT == 1 && !SW) {
+    if (p.splits > 1) {
+      launch_decode_split<MT, RT, W, U, PACKX, RANK, SW, true>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
+      return;
+    }
+  }
+  launch_decode_split<MT, RT, W, U, PACKX, RANK, SW, false>(xq, ldxq, w, ldw, M, N, K, p, partial, counters, ep, stream);
 }
 
 template <int MT, int RT, bool PACKX, int RANK, bool SW>
@@ -362,7 +396,9 @@ static hipError_t launch_decode_mt(const uint8_t* xq, int64_t ldxq, const uint8_
 hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, bool packed_x, const uint8_t* w, int64_t ldw, int M, int N, int K,
                        const DecodePlan& plan, float* partial, int* counters, const Epilogue& ep, int rank,
                        hipStream_t stream) {
-  if (M < 1 || M > kDecodeMaxRows || (rank != 0 && rank != 16) || (plan.rt != 1 && plan.rt != 2)) return hipErrorInvalidValue;
+  if (M < 1 || M > kDecodeMaxRows || (rank != 0 && rank != 16) || (plan.rt != 1 && plan.rt != 2) || plan.splits < 1 ||
+      plan.splits > kMaxDecodeSplits || (plan.splits > 1 && plan.rt != 1))
+    return hipErrorInvalidValue;
   if (ep.half) {
     // Fused SwiGLU: packed activation codes only (jv_fp8_linear_swiglu packs them), one gate/up pair per wave.
     if (!packed_x || plan.rt != 2 || plan.splits != 1 || 2 * ep.half != N || ep.half % 16) return hipErrorInvalidValue;

@@ -43,6 +43,18 @@ struct DecodePlan {
   int splits;  // workgroups along K
 };
 
+// First 128-deep k step of K slice `slice` of splits * W (the decode kernels'
+// W waves per split): floor(ksteps * slice / (splits * W)). In 32 bits, since
+// ksteps * splits * W <= K for W <= 8 and splits <= 16; without a K split the
+// divisor is the compile-time W, a shift. (A 64-bit division by a register
+// took ~130 scalar instructions, twice, ahead of every wave's first load.)
+template <int W>
+__device__ __forceinline__ int slice_begin(int ksteps, int slice, int splits) {
+  static_assert(W >= 1 && W <= 8 && (W & (W - 1)) == 0, "1-8 waves, a power of two");
+  const uint32_t num = (uint32_t)ksteps * (uint32_t)slice;
+  return (int)(splits == 1 ? num / (uint32_t)W : num / ((uint32_t)splits * W));
+}
+
 // Prefill launch shape: output tile bm (tokens) x bn (channels), a wgm x wgn
 // grid of waves per workgroup, K stages of bk bytes in a ring of `stages` LDS
 // buffers, and group_m M-tiles walking N together. pingpong selects the form

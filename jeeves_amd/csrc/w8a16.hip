@@ -27,8 +27,10 @@ __device__ __forceinline__ uint16_t w8a16_out(float acc, float swn, bool has_bia
 
 // Weights: lane l holds k bytes [32j, 32j+32) of row l%16 for j = l/16 of each
 // 128-k step; the four 16x16x32 MFMAs q of a step use k = 32j + 8q + [0, 8)
-// on both operands.
-template <int MT, int RT, int W, int U, bool PACKW>
+// on both operands. SPLIT: workgroups split K (grid.y = splits > 1); without
+// it the wave's k range takes the compile-time divisor W, as in
+// gemm_decode_kernel.
+template <int MT, int RT, int W, int U, bool PACKW, bool SPLIT>
 __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                               const uint8_t* __restrict__ w, int64_t ldw, int M, int N,
                                                               int K, int splits, float* __restrict__ partial,
@@ -42,12 +44,19 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
   // branches, never EXEC-masked regions, whose MFMAs gfx950 would still
   // execute with EXEC = 0 (see gemm_decode_kernel).
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int group = blockIdx.x, split = blockIdx.y;
+  const int group = blockIdx.x, split = SPLIT ? (int)blockIdx.y : 0;
   const int n0 = group * 16 * RT;
 
   const int ksteps = K >> 7;
-  const int slices = splits * W, slice = split * W + wave;
-  const int s_begin = (int)((int64_t)ksteps * slice / slices), s_end = (int)((int64_t)ksteps * (slice + 1) / slices);
+  int s_begin, s_end;
+  if constexpr (SPLIT) {
+    const int slice = split * W + wave;
+    s_begin = slice_begin<W>(ksteps, slice, splits);
+    s_end = slice_begin<W>(ksteps, slice + 1, splits);
+  } else {
+    s_begin = ksteps * wave / W;
+    s_end = ksteps * (wave + 1) / W;
+  }
 
   const int li = lane & 15, j32 = (lane >> 4) * 32;
   // Row-major weight rows, or the tiled fragment layout (ldw = 0): the same
@@ -86,23 +95,29 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // One base address per operand and burst, constant offsets per step.
+  constexpr int WSTEP = PACKW ? 2048 : 128;
   for (int s = s_begin; s < s_end; s += U) {
     i32x4 wa[U][RT][2];
     i32x4 xa[U][MT][4];
+    const uint8_t* wb[RT];
+    const uint16_t* xb[MT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) wb[rt] = wp[rt] + (int64_t)s * WSTEP;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xb[mt] = xp[mt] + (int64_t)s * 128;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (s + u >= s_end) break;
-      const int64_t k0 = (int64_t)(s + u) * 128;
-      const int64_t woff = PACKW ? (int64_t)(s + u) * 2048 : k0;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        wa[u][rt][0] = *reinterpret_cast<const i32x4*>(wp[rt] + woff);
-        wa[u][rt][1] = *reinterpret_cast<const i32x4*>(wp[rt] + woff + (PACKW ? 1024 : 16));
+        wa[u][rt][0] = *reinterpret_cast<const i32x4*>(wb[rt] + u * WSTEP);
+        wa[u][rt][1] = *reinterpret_cast<const i32x4*>(wb[rt] + u * WSTEP + (PACKW ? 1024 : 16));
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xa[u][mt][q] = *reinterpret_cast<const i32x4*>(xp[mt] + k0 + 8 * q);
+        for (int q = 0; q < 4; ++q) xa[u][mt][q] = *reinterpret_cast<const i32x4*>(xb[mt] + u * 128 + 8 * q);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -142,12 +157,13 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
     for (int wv = 0; wv < W; ++wv) sum += redf[wv * RT * MT * 256 + src];
     const int m = mt * 16 + ml, n = n0 + rt * 16 + nl;
     if (m < M && n < N) {
-      if (splits == 1)
+      if (!SPLIT || splits == 1)
         y[(int64_t)m * ldy + n] = w8a16_out(sum, pre_sw[j], has_bias, pre_b[j]);
       else  // device-coherent store: visible to the reducing workgroup without a cache flush
         __hip_atomic_store(partial + ((int64_t)split * M + m) * N + n, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  if constexpr (!SPLIT) return;
   if (splits == 1) return;
 
   // The workgroup that sees count splits-1 sums every split's partials in
@@ -199,12 +215,20 @@ static void launch_w8a16_decode(const uint16_t* x, int64_t ldx, const uint8_t* w
                                 uint16_t* y, int64_t ldy, hipStream_t stream) {
   constexpr int U = w8a16_unroll(MT, RT);
   const dim3 grid((unsigned)p.groups, (unsigned)p.splits), block(64 * W);
-  if (ldw == 0)
-    w8a16_decode_kernel<MT, RT, W, U, true><<<grid, block, 0, stream>>>(x, ldx, w, ldw, M, N, K, p.splits, partial,
-                                                                          counters, sw, bias, y, ldy);
-  else
-    w8a16_decode_kernel<MT, RT, W, U, false><<<grid, block, 0, stream>>>(x, ldx, w, ldw, M, N, K, p.splits, partial,
-                                                                           counters, sw, bias, y, ldy);
+#define JV_W8A16_LAUNCH(PW, SP)                                                                                \
+  w8a16_decode_kernel<MT, RT, W, U, PW, SP><<<grid, block, 0, stream>>>(x, ldx, w, ldw, M, N, K, p.splits, partial, \
+                                                                        counters, sw, bias, y, ldy)
+  // K splits come only with one tile per wave (as in launch_decode).
+  if constexpr (RT == 1) {
+    if (p.splits > 1) {
+      if (ldw == 0) JV_W8A16_LAUNCH(true, true);
+      else JV_W8A16_LAUNCH(false, true);
+      return;
+    }
+  }
+  if (ldw == 0) JV_W8A16_LAUNCH(true, false);
+  else JV_W8A16_LAUNCH(false, false);
+#undef JV_W8A16_LAUNCH
 }
 
 template <int MT>
@@ -227,7 +251,8 @@ static void launch_w8a16_decode_mt(const uint16_t* x, int64_t ldx, const uint8_t
 hipError_t w8a16_decode(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
                         const DecodePlan& p, float* partial, int* counters, const float* sw, const uint16_t* bias,
                         uint16_t* y, int64_t ldy, hipStream_t stream) {
-  if (M < 1 || M > kDecodeMaxRows || (K & 127)) return hipErrorInvalidValue;
+  if (M < 1 || M > kDecodeMaxRows || (K & 127) || p.splits < 1 || p.splits > 16 || (p.splits > 1 && p.rt != 1))
+    return hipErrorInvalidValue;
   switch ((M + 15) / 16) {
     case 1: launch_w8a16_decode_mt<1>(x, ldx, w, ldw, M, N, K, p, partial, counters, sw, bias, y, ldy, stream); break;
     case 2: launch_w8a16_decode_mt<2>(x, ldx, w, ldw, M, N, K, p, partial, counters, sw, bias, y, ldy, stream); break;
