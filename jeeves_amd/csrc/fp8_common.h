@@ -198,10 +198,21 @@ __device__ __forceinline__ void lds_barrier() {
 // ---------------------------------------------------------------------------
 // Wave64 reductions.
 // ---------------------------------------------------------------------------
+// Maximum over the wave, in every lane, by DPP moves (no LDS round trips,
+// which the ds_bpermute of __shfl_xor takes at each of its six steps):
+// row_shr 1, 2, 4, 8 leave each 16-lane row's maximum in its lane 15 (a
+// shifted-out source keeps `old` = 0, the identity of an unsigned max);
+// row_bcast:15 carries row 0's into row 1 and row 2's into row 3,
+// row_bcast:31 carries lane 31's into rows 2 and 3, so lane 63 holds the
+// wave's maximum, which readlane hands to every lane.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
-  return v;
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));  // row_shr:1
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));  // row_shr:2
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false));  // row_shr:4
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false));  // row_shr:8
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
