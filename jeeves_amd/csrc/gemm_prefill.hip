@@ -401,7 +401,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
   __shared__ int is_last;
 
   const int tiles = tiles_m * tiles_n;
-  const int split = (int)blockIdx.x / tiles;
+  const int split = SPLITK ? (int)blockIdx.x / tiles : 0;
   const int tile = (int)blockIdx.x - split * tiles;
   int tile_m, tile_n;
   tile_of(tile, tiles_m, tiles_n, group_m, tile_m, tile_n);
@@ -455,10 +455,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_prefill_kernel(const uint
     }
   }
 
-  // This workgroup's stages: [kt0, kt0 + KT) of the K / BK stages.
+  // This workgroup's stages: [kt0, kt0 + KT) of the K / BK stages, split as
+  // floor(kt_all * s / splits) (32-bit: kt_all * splits <= K); without a K
+  // split no division at all (the 64-bit division by a register it replaces
+  // sat ahead of every workgroup's first load).
   const int kt_all = K / BK;
-  const int kt0 = (int)((int64_t)kt_all * split / splits);
-  const int KT = (int)((int64_t)kt_all * (split + 1) / splits) - kt0;
+  int kt0 = 0, KT = kt_all;
+  if constexpr (SPLITK) {
+    kt0 = (int)((uint32_t)(kt_all * split) / (uint32_t)splits);
+    KT = (int)((uint32_t)(kt_all * (split + 1)) / (uint32_t)splits) - kt0;
+  }
   auto issue_stage = [&](int kt) {
     uint8_t* base = lds + (kt % STAGES) * STAGE;
     const int ktg = kt0 + kt;
