@@ -212,7 +212,7 @@ int jv_fp8_quantize_swiglu_output(const void* h, int64_t ldh, const uint16_t* h_
  * two 1 KB halves (h = (k%32)/16), each 64 lanes x 16 bytes with
  * lane = n%16 + 16*((k%128)/32); byte offset
  *   ((t*(K/128) + s)*2 + h)*1024 + lane*16 + k%16.
- * It needs N % 16 == 0 and K % 128 == 0 and holds N*K bytes; decode waves
+ * It needs N % 16 == 0, K % 128 == 0 and N*K < 64 GiB, and holds N*K bytes; decode waves
  * read it as one contiguous 1 KB per load. No counterpart in the reference's
  * CUDA path; its Metal path stores its weights tiled for its own kernel in
  * the same way (MetalFP8Linear.tiled_codes, inference/fp8_metal.py:13-34;

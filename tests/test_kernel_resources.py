@@ -11,7 +11,13 @@
 * no kernel serializes its global loads: a load followed at once by a wait
   for every outstanding load, repeated, is what a load guarded one at a time
   next to its use compiles to (the quantizer's per-chunk loads were, one
-  memory round trip per chunk).
+  memory round trip per chunk);
+* no kernel divides 64-bit integers by a run-time value: the expansion
+  (~130 instructions, recognisable by its 2^32 and 2^-32 float constants)
+  sat ahead of the first load of every workgroup in the decode and lockstep
+  prefill kernels, whose K-split ranges were computed that way (1 us of a
+  19 us decode GEMM, with the address arithmetic of its bursts); and every
+  kernel issues its first global load within 450 instructions of its entry.
 """
 
 from __future__ import annotations
@@ -192,3 +198,79 @@ def test_scan_finds_serialized_loads():
 \ts_waitcnt vmcnt(0)
 """
     assert serialized_loads(listing) == {"kern": 1}
+
+
+def instructions_before_first_load(asm: str) -> dict[str, int]:
+    """Per function, the instructions (labels, comments and directives not
+    counted) ahead of its first global or buffer load; functions without one
+    are left out."""
+    counts: dict[str, int] = {}
+    fn, n = None, 0
+    for line in asm.splitlines():
+        t = line.strip()
+        if (m := FUNCTION_LABEL.match(t)) and not m.group(1).startswith(".L"):
+            fn, n = m.group(1), 0
+        elif fn is None or fn in counts or not t or t.startswith((";", ".")) or t.endswith(":"):
+            continue
+        elif t.startswith(("global_load", "buffer_load")):
+            counts[fn] = n
+        else:
+            n += 1
+    return counts
+
+
+def test_every_kernel_loads_early(device_builds):
+    late = {}
+    for src, (_, asm) in device_builds.items():
+        for fn, n in instructions_before_first_load(asm).items():
+            if n > 450:
+                late[f"{src}:{fn[:80]}"] = n
+    assert not late, late
+
+
+def test_scan_counts_instructions_before_the_first_load():
+    listing = """kern:
+\ts_load_dwordx4 s[4:7], s[0:1], 0x0
+.LBB0_1:
+\t; a comment
+\ts_waitcnt lgkmcnt(0)
+\tglobal_load_dwordx4 v[2:5], v1, s[2:3]
+\tglobal_load_dwordx4 v[6:9], v1, s[2:3]
+other:
+\ts_endpgm
+"""
+    assert instructions_before_first_load(listing) == {"kern": 2}
+
+
+DIV64_CONSTANTS = re.compile(r"0x4f800000|0x2f800000")
+
+
+def divisions_64(asm: str) -> dict[str, int]:
+    """Per function, the uses of 2^32 and 2^-32 as float constants: the
+    float-reciprocal steps of a 64-bit integer division by a register."""
+    counts: dict[str, int] = {}
+    fn = None
+    for line in asm.splitlines():
+        if (m := FUNCTION_LABEL.match(line.strip())) and not m.group(1).startswith(".L"):
+            fn = m.group(1)
+        elif fn and DIV64_CONSTANTS.search(line):
+            counts[fn] = counts.get(fn, 0) + 1
+    return counts
+
+
+def test_no_kernel_divides_64_bit_integers(device_builds):
+    bad = {f"{src}:{fn[:80]}": n for src, (_, asm) in device_builds.items() for fn, n in divisions_64(asm).items()}
+    assert not bad, bad
+
+
+def test_scan_finds_a_64_bit_division():
+    listing = """kern:
+\tv_cvt_f32_u32_e32 v2, s5
+\tv_madmk_f32 v2, v3, 0x4f800000, v2
+\tv_rcp_f32_e32 v2, v2
+\tv_mul_f32_e32 v3, 0x2f800000, v2
+other:
+\tv_rcp_iflag_f32_e32 v1, v1
+\tv_mul_f32_e32 v1, 0x4f7ffffe, v1
+"""
+    assert divisions_64(listing) == {"kern": 2}
