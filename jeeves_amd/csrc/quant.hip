@@ -43,10 +43,9 @@ __global__ __launch_bounds__(THREADS) void quant_rows_bf16_kernel(
     uint8_t* __restrict__ codes, int64_t ldc, float* __restrict__ scales, uint16_t* __restrict__ h_out, int64_t ldh,
     const uint16_t* __restrict__ lora_a, float* __restrict__ lora_t) {
   __shared__ uint32_t lds[quant_row_lds_bytes<THREADS, RANK>() / 4];
-  const int row = XCD_ROWS ? packed_tile_row((int)blockIdx.x, (M + 15) >> 4) : (int)blockIdx.x;
-  if (row < 0) return;
-  quant_row<THREADS, NC, SWIGLU, RANK, PACKED>(row, x, ldx, up, ldu, K, M, codes, ldc, scales, h_out, ldh, lora_a, lora_t,
-                                               lds);
+  const int prow = XCD_ROWS ? packed_tile_row((int)blockIdx.x, (M + 15) >> 4) : (int)blockIdx.x;
+  quant_row<THREADS, NC, SWIGLU, RANK, PACKED>(max(prow, 0), x, ldx, up, ldu, K, M, codes, ldc, scales, h_out, ldh, lora_a,
+                                               lora_t, lds, prow >= 0);
 }
 
 // Rows longer than the register cache: two passes over the row (the second

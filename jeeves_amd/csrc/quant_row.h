@@ -65,16 +65,18 @@ __device__ __forceinline__ void quant_row(int row, const uint16_t* __restrict__ 
                                           const uint16_t* __restrict__ up, int64_t ldu, int K, int M,
                                           uint8_t* __restrict__ codes, int64_t ldc, float* __restrict__ scales,
                                           uint16_t* __restrict__ h_out, int64_t ldh, const uint16_t* __restrict__ lora_a,
-                                          float* __restrict__ lora_t, uint32_t* lds) {
+                                          float* __restrict__ lora_t, uint32_t* lds, bool active = true) {
   constexpr int NW = THREADS / 64;
   const int tid = threadIdx.x;
   const int nchunks = K >> 3;
-  if (PACKED && row >= M) {
-    for (int c = tid; c < nchunks; c += THREADS)
-      *reinterpret_cast<uint2*>(codes + packed_x_offset(row, c * 8, K >> 7)) = uint2{0u, 0u};
-    return;
-  }
-  const uint16_t* xr = x + (int64_t)row * ldx;
+  // A padding row of a packed tile (row >= M) runs the same path on the last
+  // real row and stores zero codes, no scale; an inactive workgroup (past the
+  // last tile) stores nothing. With no branch ahead of the loads, the kernel's
+  // argument loads go out together (one scalar round trip before the first
+  // row load instead of two).
+  const bool real = active && (!PACKED || row < M);
+  const int src = PACKED ? min(row, M - 1) : row;
+  const uint16_t* xr = x + (int64_t)src * ldx;
   uint4 v[NC];
   uint32_t am = 0;
   float t[RANK > 0 ? RANK : 1];
@@ -89,7 +91,7 @@ __device__ __forceinline__ void quant_row(int row, const uint16_t* __restrict__ 
   for (int i = 0; i < NC; ++i) {
     const int64_t c = min(tid + i * THREADS, nchunks - 1);
     v[i] = *reinterpret_cast<const uint4*>(xr + c * 8);
-    if constexpr (SWIGLU) u[i] = *reinterpret_cast<const uint4*>(up + (int64_t)row * ldu + c * 8);
+    if constexpr (SWIGLU) u[i] = *reinterpret_cast<const uint4*>(up + (int64_t)src * ldu + c * 8);
   }
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
@@ -98,7 +100,7 @@ __device__ __forceinline__ void quant_row(int row, const uint16_t* __restrict__ 
       v[i] = uint4{swiglu_pair(v[i].x, u[i].x), swiglu_pair(v[i].y, u[i].y), swiglu_pair(v[i].z, u[i].z),
                    swiglu_pair(v[i].w, u[i].w)};
     if (c < nchunks) {
-      if (SWIGLU && h_out) *reinterpret_cast<uint4*>(h_out + (int64_t)row * ldh + (int64_t)c * 8) = v[i];
+      if (SWIGLU && h_out && real) *reinterpret_cast<uint4*>(h_out + (int64_t)row * ldh + (int64_t)c * 8) = v[i];
     } else {
       v[i] = uint4{0, 0, 0, 0};
     }
@@ -141,7 +143,7 @@ __device__ __forceinline__ void quant_row(int row, const uint16_t* __restrict__ 
 #pragma unroll
   for (int wv = 1; wv < NW; ++wv) amax_bits = max(amax_bits, lds[wv]);
   const float scale = scale_from_amax_bits(amax_bits);
-  if (tid == 0) scales[row] = scale;
+  if (tid == 0 && real) scales[row] = scale;
   const bool fast = amax_bits < 0x7F80u;  // finite row: scale finite and > 0
   const float r = 1.0f / scale;
   uint8_t* cr = codes + (PACKED ? 0 : (int64_t)row * ldc);
@@ -150,7 +152,7 @@ __device__ __forceinline__ void quant_row(int row, const uint16_t* __restrict__ 
     const int c = tid + i * THREADS;
     if (c < nchunks) {
       const int64_t off = PACKED ? packed_x_offset(row, c * 8, K >> 7) : (int64_t)c * 8;
-      *reinterpret_cast<uint2*>(cr + off) = encode8(v[i], scale, r, fast);
+      if (active) *reinterpret_cast<uint2*>(cr + off) = real ? encode8(v[i], scale, r, fast) : uint2{0u, 0u};
     }
   }
   if constexpr (RANK > 0) {
@@ -161,7 +163,7 @@ __device__ __forceinline__ void quant_row(int row, const uint16_t* __restrict__ 
       if (lane == 0) tred[wave * RANK + q] = s;
     }
     __syncthreads();
-    if (tid < RANK) {
+    if (tid < RANK && real) {
       float sum = tred[tid];
 #pragma unroll
       for (int wv = 1; wv < NW; ++wv) sum += tred[wv * RANK + tid];
