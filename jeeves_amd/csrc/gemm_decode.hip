@@ -309,9 +309,9 @@ DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count, bool swigl
   if (!swiglu && tiles > cu_count && tiles <= 2 * (int64_t)cu_count && K / 128 >= 16) p.rt = 2;
   // Two tiles per wave stream best as eight waves of four k steps rather than
   // four waves of eight (gate+up 19.2 -> 18.5 us at M = 1, 20.0 -> 19.7 at
-  // 16), except with the SwiGLU epilogue, whose gate/up pairing keeps four
-  // (quantizer + GEMM 23.1 us with four waves, 24.3 with eight).
-  if (!swiglu && p.rt == 2 && K / 128 >= 16) p.waves = 8;
+  // 16), the SwiGLU epilogue's gate/up pairs too (decode layer step at M = 16
+  // 60.8 -> 60.6 us in same-box A/B runs).
+  if (p.rt == 2 && K / 128 >= 16) p.waves = 8;
   p.unroll = decode_unroll((int)mt, p.rt, p.waves);
   const int64_t groups = (tiles + p.rt - 1) / p.rt;
   p.groups = (int)groups;
