@@ -134,6 +134,22 @@ def layer_shapes(synthetic) -> dict[str, tuple[int, int]]:
     return {"qkv": (s["q"][0] + s["k"][0] + s["v"][0], s["q"][1]), "o": s["o"], "gate_up": s["gate_up"], "down": s["down"]}
 
 
+# The 9B model's merged projections on K = 4096 (inference/engine.py:154-165):
+# an attention layer's q+gate, k and v (10240), a DeltaNet layer's qkv (8192),
+# and the drafter's q/k/v (drafter/view.py:41-53, 12288).
+MERGED_9B = {"qkv_attention_10240": 10240, "qkv_deltanet_8192": 8192, "qkv_drafter_12288": 12288}
+
+
+def merged_9b_weights(torch, synthetic, quantize_rows) -> dict:
+    from jeeves_amd.fp8 import tile_weight
+
+    w = {}
+    for i, (name, N) in enumerate(MERGED_9B.items()):
+        wq, sw = quantize_rows(synthetic.weight(N, synthetic.HIDDEN, 900 + i).cuda())
+        w[name] = (tile_weight(wq), sw)
+    return w
+
+
 def make_weights(torch, synthetic, quantize_rows) -> dict:
     """Tiled e4m3 codes and scales of the six projections (the decode and
     prefill workloads' weights), plus q/k/v merged the way FP8Linear.concatenated
@@ -279,13 +295,15 @@ def six_step_ms(b: Bench, torch, fp8, synthetic, weights, case, M: int, replays:
     return ms
 
 
-def per_kernel(b, torch, fp8, synthetic, rot, M: int, case, replays: int, bound: str) -> dict:
+def per_kernel(b, torch, fp8, synthetic, rot, M: int, case, replays: int, bound: str, shapes: dict | None = None) -> dict:
     """GEMM kernel time per projection at M tokens (and the merged q/k/v), with
-    GB/s or TFLOP/s and the fraction of the bound's peak."""
+    GB/s or TFLOP/s and the fraction of the bound's peak; `shapes` ({name:
+    (N, K)}, K = 4096 activations) replaces the projection list."""
     out = {}
-    shapes = dict(synthetic.SHAPES, **{"qkv": layer_shapes(synthetic)["qkv"]})
+    if shapes is None:
+        shapes = dict(synthetic.SHAPES, **{"qkv": layer_shapes(synthetic)["qkv"]})
     for name, (N, K) in shapes.items():
-        x = case("q" if name == "qkv" else name, M)[0].cuda()
+        x = case(name if name in synthetic.SHAPES else "q", M)[0].cuda()
         ms = kernel_ms(b, fp8, rot.copies(name), quantized_operands(torch, fp8, x), replays)
         if bound == "hbm":
             gbs = linear_bytes(M, N, K) / (ms * 1e-3) / 1e9
@@ -589,6 +607,12 @@ def main() -> int:
     k_bytes = linear_bytes(M, N, Kg)
     k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
     log(f"bench: decode GEMM kernels {kernels}")
+    merged_shapes = {name: (N9, synthetic.HIDDEN) for name, N9 in MERGED_9B.items()}
+    merged = {}
+    if not args.no_sweep:
+        weights.update(merged_9b_weights(torch, synthetic, quantize_rows))
+        merged = per_kernel(b, torch, fp8, synthetic, rot, M, synthetic.decode_case, 40, "hbm", merged_shapes)
+        log(f"bench: 9B merged projections {merged}")
     sweep = {}
     if not args.no_sweep:
         for m in DECODE_SWEEP_ROWS:
@@ -629,6 +653,7 @@ def main() -> int:
                                      "GB/s": round(six_bytes / (six_ms * 1e-3) / 1e9, 1),
                                      "note": "q, k, v, o, gate+up, down each with its own quantizer launch"},
             "kernels_m16": kernels,
+            "kernels_m16_9b_merged": merged,
             "kernels_sweep": sweep,
         },
     }
@@ -648,6 +673,8 @@ def main() -> int:
         if not args.no_sweep:
             for m in PREFILL_SWEEP_ROWS:
                 psweep[f"m{m}"] = per_kernel(b, torch, fp8, synthetic, rot, m, synthetic.prefill_case, 4, "mfma")
+            psweep[f"m{Mp}_9b_merged"] = per_kernel(b, torch, fp8, synthetic, rot, Mp, synthetic.prefill_case, 8, "mfma",
+                                                     merged_shapes)
         result["prefill"] = {
             "tokens": Mp, "ms_per_step": round(pms, 4), "TFLOP/s": round(lflops / (pms * 1e-3) / 1e12, 1),
             "step": "the decode step's layer (q/k/v merged, o, gate+up with SwiGLU epilogue, quantization of h, down) at M=2048",

@@ -91,6 +91,24 @@ def test_decode_workload_shapes(name, M):
         assert torch.equal(y, yq)
 
 
+# The 9B model's merged projections on K = 4096 (inference/engine.py:154-165):
+# an attention layer's q+gate, k and v (N = 10240), a DeltaNet layer's qkv
+# (8192), the drafter's q/k/v (drafter/view.py:41-53, 12288); tiled as
+# FP8Linear.concatenated keeps them, across the decode and prefill plans.
+# Sampled token rows against the oracle, and every output equal to the same
+# GEMM on row-major codes.
+@pytest.mark.parametrize("N", [8192, 10240, 12288])
+@pytest.mark.parametrize("M", [1, 16, 64, 128, 2048])
+def test_9b_merged_projection_widths(weights, N, M):
+    K = 4096
+    wq, sw = weights(N, K)
+    x = synthetic.activations_outliers(M, K, 9000 + M).cuda()
+    y = fp8_matmul(x, tile_weight(wq), sw, tiled=True)
+    rows = torch.arange(0, M, max(1, M // 16), device="cuda")
+    check(y[rows], x[rows], wq, sw)
+    assert torch.equal(y, fp8_matmul(x, wq, sw))
+
+
 @pytest.mark.parametrize("N", [24576, 24592])
 @pytest.mark.parametrize("M", [17, 24, 40, 64])
 def test_wide_small_batches_take_64x64_prefill_tiles(N, M):
