@@ -227,8 +227,9 @@ def layer_inputs(synthetic, M: int, K: int, case) -> dict:
 def layer_linears(fp8, synthetic, xs, weights, lora=None):
     """One decoder layer's linear stack. With `xs` a dict (attention input,
     attention output, MLP input) and merged q/k/v weights: the engine's merged
-    qkv projection, o, gate+up with SwiGLU in its epilogue (h), the down
-    projection's quantization of h, down. With `xs` one tensor: q, k, v
+    qkv projection, o, gate+up with SwiGLU in its epilogue (h, and at decode
+    sizes its per-16-channel maxima), the down projection's quantization of
+    h, down. With `xs` one tensor: q, k, v
     (separate, each with its own LoRA adapter when `lora` is given), o and
     gate+up all on it, then the same SwiGLU and down."""
     if isinstance(xs, dict):
@@ -243,8 +244,11 @@ def layer_linears(fp8, synthetic, xs, weights, lora=None):
             wq, sw = weights[name]
             fp8.fp8_matmul(h, wq, sw, tiled=True, lora=lora[name] if lora else None)
     wq, sw = weights["gate_up"]
-    hh = fp8.gate_up_swiglu(h, wq, sw, tiled=True, lora=lora["gate_up"] if lora else None)
-    res = fp8.quantize_swiglu_output(hh, lora_a=lora["down"][0] if lora else None, packed=True)
+    # Decode batches without LoRA quantize h from the epilogue's maxima (as FP8SwiGLU does).
+    amax = not lora and h.shape[0] <= fp8.DECODE_MAX_ROWS
+    out = fp8.gate_up_swiglu(h, wq, sw, tiled=True, lora=lora["gate_up"] if lora else None, amax=amax)
+    hh, parts = out if amax else (out, None)
+    res = fp8.quantize_swiglu_output(hh, parts, lora_a=lora["down"][0] if lora else None, packed=True)
     wq, sw = weights["down"]
     return fp8.fp8_matmul_quantized(res[0], res[1], wq, sw, lora_t=res[2] if lora else None,
                                     lora_b=lora["down"][1] if lora else None,

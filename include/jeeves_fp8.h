@@ -198,10 +198,14 @@ int jv_fp8_linear_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw,
  * semantics, as jv_fp8_quantize_rows_bf16), for jv_fp8_gemm: codes in the
  * packed fragment order when ldc = 0, scales [M]; with lora_a [rank, I] bf16
  * also lora_t [M, rank] = h A^T in fp32. h_amax: the maxima
- * jv_fp8_linear_swiglu wrote for this h, or NULL; it is not read: each row's
- * maximum is taken from h itself in the one pass that encodes it (the row
- * stays in registers), which is as fast as reading the maxima would be. I a
- * multiple of 16 (of 128 when packed), at most 16384. */
+ * jv_fp8_linear_swiglu wrote for this h, or NULL. Decode batches (M <= 64)
+ * in the packed layout without LoRA take each row's maximum from h_amax when
+ * it is 8-byte aligned, so a row splits over several workgroups; h_amax must
+ * then be exactly what jv_fp8_linear_swiglu stored with this h. Otherwise it
+ * is not read, and each row's maximum is taken from h itself in the one pass
+ * that encodes it (the row stays in registers). Either way the codes and
+ * scales are the same bits. I a multiple of 16 (of 128 when packed), at most
+ * 16384. */
 int jv_fp8_quantize_swiglu_output(const void* h, int64_t ldh, const uint16_t* h_amax, int64_t M, int64_t I, void* codes,
                                   int64_t ldc, float* scales, const void* lora_a, int64_t lora_rank, float* lora_t,
                                   void* stream);

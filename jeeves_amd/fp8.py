@@ -424,8 +424,11 @@ def quantize_swiglu_output(h: torch.Tensor, amax: torch.Tensor | None = None, *,
     ``(codes, scales)``, plus ``t = h A^T`` (float32 [M,r]) with ``lora_a``.
     ``packed``: codes as a flat uint8 buffer in the GEMMs' fragment order (for
     ``fp8_matmul_quantized(..., packed_rows=M)``); ``amax``: the maxima
-    ``gate_up_swiglu(..., amax=True)`` returned with h, accepted but not read
-    (each row's maximum comes from h in the same pass that encodes it)."""
+    ``gate_up_swiglu(..., amax=True)`` returned with this h, or None. Decode
+    batches (M <= 64) in the packed layout without LoRA read each row's
+    maximum from them, so a row splits over several workgroups; elsewhere
+    they are not read (each row's maximum comes from h in the pass that
+    encodes it). The result is the same bits either way."""
     M, I = h.shape
     dev = h.device
     if dev.type != "cuda" or h.dtype != torch.bfloat16:
@@ -615,9 +618,12 @@ class FP8SwiGLU(nn.Module):
         packed = M > 0 and inter % BLOCK_K == 0 and inter <= QUANT_MAX_PACKED_COLS
         if self.gate_up.activations == "fp8" and self.fused():
             w, tiled = self.gate_up.kernel_weight()
-            h = gate_up_swiglu(x2.to(torch.bfloat16), w, self.gate_up.scale, bias=self.gate_up.bias,
-                               lora=self.gate_up.lora, tiled=tiled)
-            out = quantize_swiglu_output(h, lora_a=lora_a, packed=packed)
+            # Decode batches quantize h from the epilogue's maxima.
+            amax = packed and lora_a is None and M <= DECODE_MAX_ROWS
+            res = gate_up_swiglu(x2.to(torch.bfloat16), w, self.gate_up.scale, bias=self.gate_up.bias,
+                                 lora=self.gate_up.lora, tiled=tiled, amax=amax)
+            h, parts = res if amax else (res, None)
+            out = quantize_swiglu_output(h, parts, lora_a=lora_a, packed=packed)
         else:
             gu = self.gate_up(x2)
             out = swiglu_quantize(gu[:, :inter], gu[:, inter:], lora_a=lora_a, packed=packed)

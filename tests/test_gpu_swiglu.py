@@ -105,6 +105,51 @@ def test_quantize_swiglu_output_equals_quantize_rows(M, rank):
         assert torch.equal(packed[2], out[2])
 
 
+@pytest.mark.parametrize("I", [128, 1024, 4096, 12288, 16384])
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 40, 64])
+def test_quantize_h_from_maxima_equals_one_pass(I, M):
+    """Decode batches quantize h from the epilogue's per-16-channel maxima,
+    each row split over workgroups: codes (padding rows included) and scales
+    are the bits of the one-pass quantizer, which takes each row's maximum
+    from h. Rows whose maximum sits in the first or last 16 channels, an inf,
+    a NaN and an all-zero row."""
+    print(f"h from maxima I={I} M={M}", flush=True)
+    h = synthetic.activations_heavy_tail(M, I, 8500 + M + I)
+    h[0, -1] = 300.0
+    if M > 1:
+        h[1, 0] = -300.0
+    if M > 4:
+        h[2, I // 2] = float("inf")
+        h[3, 7] = float("nan")
+        h[4] = 0.0
+    h = h.cuda()
+    parts = torch.from_numpy(amax_of(h).view(np.int16)).cuda()
+    want = quantize_swiglu_output(h, packed=True)
+    got = quantize_swiglu_output(h, parts, packed=True)
+    assert torch.equal(got[0], want[0]), (I, M)
+    assert helpers.same_f32(got[1].cpu().numpy(), want[1].cpu().numpy()).all(), (I, M)
+    codes, scales = quantize_rows(h)
+    assert helpers.same_f32(got[1].cpu().numpy(), scales.cpu().numpy()).all(), (I, M)
+
+
+@pytest.mark.parametrize("M", [1, 16, 64])
+def test_quantize_h_from_epilogue_maxima(M):
+    """The maxima gate_up_swiglu stores, fed to the quantizer of h, give the
+    bits of the quantizer that reads h alone; also through a misaligned view
+    of the maxima (not 8-byte aligned: the one-pass path)."""
+    I, K = 12288, 4096
+    x = synthetic.activations_outliers(M, K, 8600 + M).cuda()
+    wq, sw = quantize_rows(synthetic.weight(2 * I, K, 8601).cuda())
+    h, parts = gate_up_swiglu(x, tile_weight(wq), sw, tiled=True, amax=True)
+    want = quantize_swiglu_output(h, packed=True)
+    got = quantize_swiglu_output(h, parts, packed=True)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+    shifted = torch.empty(M * (I // 16) + 1, dtype=torch.int16, device="cuda")[1:].view(M, I // 16)
+    shifted.copy_(parts)
+    got = quantize_swiglu_output(h, shifted, packed=True)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+
+
 @pytest.mark.parametrize("M", [1, 16, 64, 512])
 def test_fp8_swiglu_module_fused_equals_steps(M):
     """FP8SwiGLU's fused forward equals gate+up (FP8Linear), SwiGLU on bf16 and
