@@ -132,6 +132,24 @@ def test_quantize_h_from_maxima_equals_one_pass(I, M):
     assert helpers.same_f32(got[1].cpu().numpy(), scales.cpu().numpy()).all(), (I, M)
 
 
+@pytest.mark.parametrize("M", [1, 64, 65, 300])
+def test_maxima_are_read_only_for_decode_batches(M):
+    """The dispatch: maxima that understate every row (all zero) change the
+    scales exactly where the quantizer reads them (M <= 64, packed, no LoRA)
+    and nowhere else, so the decode path really takes its maximum from them."""
+    I = 4096
+    h = synthetic.activations_heavy_tail(M, I, 8700 + M).cuda()
+    zeros = torch.zeros(M, I // 16, dtype=torch.int16, device="cuda")
+    want = quantize_swiglu_output(h, packed=True)
+    got = quantize_swiglu_output(h, zeros, packed=True)
+    read = M <= 64
+    assert torch.equal(got[1], want[1]) != read, M
+    # LoRA and row-major codes never read the maxima
+    a = synthetic.lora_factors(4096, I, 8701)[0].cuda()
+    assert torch.equal(quantize_swiglu_output(h, zeros, lora_a=a, packed=True)[1], want[1])
+    assert torch.equal(quantize_swiglu_output(h, zeros, packed=False)[1], want[1])
+
+
 @pytest.mark.parametrize("M", [1, 16, 64])
 def test_quantize_h_from_epilogue_maxima(M):
     """The maxima gate_up_swiglu stores, fed to the quantizer of h, give the
