@@ -192,7 +192,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
     // h[m, hc] = bf16(bf16(silu(y_gate)) * y_up), y = the bf16 outputs the
     // unfused GEMM would store; thread groups of 16 (one token, 16 channels)
     // also take the largest |h| for the row's quantizer. Every break and
-    // shuffle below is uniform across a wave (kOut and kThreads are multiples
+    // DPP row maximum below is uniform across a wave (kOut and kThreads are multiples
     // of 64).
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
@@ -219,10 +219,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_decode_kernel(const uint8_t* 
         ep.y[(int64_t)m * ep.ldy + hc] = (uint16_t)hv;
       }
       if (ep.parts) {
-        uint32_t mx = hv & 0x7FFFu;
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
-        if (nl == 0 && m < M) ep.parts[(int64_t)m * (ep.half >> 4) + (hc >> 4)] = (uint16_t)mx;
+        // The 16 channels nl = 0..15 of token m are one 16-lane DPP row.
+        const uint32_t mx = row16_max_u32_in_lane15(hv & 0x7FFFu);
+        if (nl == 15 && m < M) ep.parts[(int64_t)m * (ep.half >> 4) + (hc >> 4)] = (uint16_t)mx;
       }
     }
     return;
