@@ -57,6 +57,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "FP8 linear TFLOP/s (M=2048) and HBM GB/s (M<=16) on 1 MI355X; % of roofline"
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 512 << 20
 LAUNCHES_PER_GRAPH = 24
 # Decode batch sizes besides 16: the other decode rows of the decode workload,
@@ -64,6 +65,7 @@ LAUNCHES_PER_GRAPH = 24
 # to a power of two, inference/engine.py:299-306).
 DECODE_SWEEP_ROWS = (1, 4, 32, 64, 96, 128)
 PREFILL_SWEEP_ROWS = (512, 8192)
+W8A16_ROWS = (1, 16, 64, 2048)
 PMC_SUMMARY = "profiles/gemm_decode_prefill_pmc.md"
 
 
@@ -196,21 +198,29 @@ def quantized_operands(torch, fp8, x):
     return codes, sx, M
 
 
-def kernel_ms(b: Bench, fp8, copies, operands, replays: int, graphs: int = 4) -> float:
-    """Average time (ms) of one GEMM kernel launch on the activation codes
-    fp8_matmul would produce, from graphs of back-to-back launches on the bench
-    stream over rotated weight copies."""
-    xq, sx, packed_rows = operands
+def launches_ms(b: Bench, copies, launch, replays: int, graphs: int = 4) -> float:
+    """Average time (ms) of one launch(wq, sw), from graphs of
+    LAUNCHES_PER_GRAPH back-to-back launches on the bench stream over rotated
+    weight copies."""
     gs = []
     for c in range(min(len(copies), graphs)):
         def launches(c=c):
             for j in range(LAUNCHES_PER_GRAPH):
-                wq, sw = copies[(c * LAUNCHES_PER_GRAPH + j) % len(copies)]
-                fp8.fp8_matmul_quantized(xq, sx, wq, sw, packed_rows=packed_rows, tiled=True)
+                launch(*copies[(c * LAUNCHES_PER_GRAPH + j) % len(copies)])
         gs.append(b.capture(launches))
     ms = b.time_graphs(gs, replays, 3) / LAUNCHES_PER_GRAPH
     del gs
     return ms
+
+
+def kernel_ms(b: Bench, fp8, copies, operands, replays: int, graphs: int = 4, tiled: bool = True) -> float:
+    """Average time (ms) of one GEMM kernel launch on the activation codes
+    fp8_matmul would produce, from graphs of back-to-back launches on the bench
+    stream over rotated weight copies (tiled: FP8Linear's tiled copy; else the
+    row-major codes, the layout FP8Linear.TILED_COPY = False reads)."""
+    xq, sx, packed_rows = operands
+    return launches_ms(b, copies, lambda wq, sw: fp8.fp8_matmul_quantized(xq, sx, wq, sw, packed_rows=packed_rows,
+                                                                             tiled=tiled), replays, graphs)
 
 
 def layer_inputs(synthetic, M: int, K: int, case) -> dict:
@@ -299,22 +309,95 @@ def six_step_ms(b: Bench, torch, fp8, synthetic, weights, case, M: int, replays:
     return ms
 
 
-def per_kernel(b, torch, fp8, synthetic, rot, M: int, case, replays: int, bound: str, shapes: dict | None = None) -> dict:
+def rate(M: int, N: int, K: int, ms: float, bound: str, mfma_peak: float = None) -> dict:
+    """Time, throughput and roofline fraction of one linear call: GB/s of its
+    algorithmic bytes against 8 TB/s ("hbm"), or TFLOP/s against the MFMA
+    peak ("mfma"; FP8 unless given)."""
+    if bound == "hbm":
+        gbs = linear_bytes(M, N, K) / (ms * 1e-3) / 1e9
+        return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+    peak = mfma_peak or FP8_PEAK_TFLOPS
+    key = "frac_of_fp8_peak" if peak == FP8_PEAK_TFLOPS else "frac_of_bf16_peak"
+    return {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1), key: round(tf / peak, 4)}
+
+
+def per_kernel(b, torch, fp8, synthetic, rot, M: int, case, replays: int, bound: str, shapes: dict | None = None,
+               tiled: bool = True) -> dict:
     """GEMM kernel time per projection at M tokens (and the merged q/k/v), with
     GB/s or TFLOP/s and the fraction of the bound's peak; `shapes` ({name:
-    (N, K)}, K = 4096 activations) replaces the projection list."""
+    (N, K)}, K = 4096 activations) replaces the projection list; `tiled`
+    False times the row-major weights of `rot`."""
     out = {}
     if shapes is None:
         shapes = dict(synthetic.SHAPES, **{"qkv": layer_shapes(synthetic)["qkv"]})
     for name, (N, K) in shapes.items():
         x = case(name if name in synthetic.SHAPES else "q", M)[0].cuda()
-        ms = kernel_ms(b, fp8, rot.copies(name), quantized_operands(torch, fp8, x), replays)
-        if bound == "hbm":
-            gbs = linear_bytes(M, N, K) / (ms * 1e-3) / 1e9
-            out[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
-        else:
-            tf = 2 * M * N * K / (ms * 1e-3) / 1e12
-            out[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
+        ms = kernel_ms(b, fp8, rot.copies(name), quantized_operands(torch, fp8, x), replays, tiled=tiled)
+        out[name] = rate(M, N, K, ms, bound)
+    return out
+
+
+def per_kernel_w8a16(b, torch, fp8, synthetic, rot, M: int, case, replays: int) -> dict:
+    """The W8A16 parity mode (the reference's own arithmetic: bf16 activations
+    times e4m3 weights widened to bf16, bf16 MFMA, fp32 sums) per projection at
+    M tokens: GB/s against 8 TB/s at decode sizes (M <= 64), TFLOP/s against
+    the dense bf16 MFMA peak (2.5 PFLOP/s) above."""
+    out = {}
+    for name, (N, K) in synthetic.SHAPES.items():
+        x = case(name, M)[0].cuda()
+        ms = launches_ms(b, rot.copies(name), lambda wq, sw: fp8.fp8_matmul_w8a16(x, wq, sw, tiled=True), replays)
+        out[name] = rate(M, N, K, ms, "hbm" if M <= 64 else "mfma", BF16_PEAK_TFLOPS)
+    return out
+
+
+def mlp_steps(b: Bench, torch, fp8, synthetic, weights, M: int, replays: int) -> dict:
+    """The MLP block (gate, up, SwiGLU, down) at M tokens, two ways, over rotated
+    weight copies (HIP graph replay):
+    * reference_shaped: what the reference's SwiGLU.forward runs after the
+      import swap alone (model/model.py:581-584): gate and up as two FP8Linear
+      calls (N = 12288 each, each quantizing x), torch's F.silu(gate) * up on
+      bf16, then down (quantizing h);
+    * fused: FP8SwiGLU, which fuse_swiglus puts in its place: one gate+up GEMM
+      with SwiGLU in its epilogue, the quantization of h from the epilogue's
+      maxima, the down GEMM.
+    GB/s counts the same algorithmic bytes for both (gate+up and down linears)."""
+    import torch.nn.functional as F
+
+    I = synthetic.INTERMEDIATE
+    x = synthetic.decode_case("gate_up", M)[0].cuda()
+    gu, sgu = weights["gate_up"]
+    dw, sd = weights["down"]
+    per_copy = gu.numel() + dw.numel()
+    n = max(2, -(-ROTATE_BYTES // per_copy) + 1)
+    sets = [(gu, sgu, dw, sd)] + [(gu.clone(), sgu, dw.clone(), sd) for _ in range(n - 1)]
+
+    def reference_shaped(s):
+        g_, sg_, d_, sd_ = s
+        # the tiled layout keeps whole 16-row tiles in row order: the first I rows are gate_proj's tiled codes
+        gate = fp8.fp8_matmul(x, g_[:I], sg_[:I], tiled=True)
+        up = fp8.fp8_matmul(x, g_[I:], sg_[I:], tiled=True)
+        h = F.silu(gate) * up
+        fp8.fp8_matmul(h, d_, sd_, tiled=True)
+
+    def fused(s):
+        g_, sg_, d_, sd_ = s
+        amax = M <= fp8.DECODE_MAX_ROWS
+        out = fp8.gate_up_swiglu(x, g_, sg_, tiled=True, amax=amax)
+        hh, parts = out if amax else (out, None)
+        res = fp8.quantize_swiglu_output(hh, parts, packed=True)
+        fp8.fp8_matmul_quantized(res[0], res[1], d_, sd_, packed_rows=M, tiled=True)
+
+    nbytes = linear_bytes(M, 2 * I, synthetic.HIDDEN) + linear_bytes(M, synthetic.HIDDEN, I)
+    out = {}
+    for name, fn in (("reference_shaped", reference_shaped), ("fused", fused)):
+        graphs = [b.capture(lambda s=s, fn=fn: fn(s)) for s in sets]
+        ms = b.time_graphs(graphs, replays, 3)
+        del graphs
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    del sets
+    torch.cuda.empty_cache()
     return out
 
 
@@ -431,6 +514,77 @@ def pmc_driver(torch, fp8, synthetic, quantize_rows, launches: int = 6) -> None:
         fp8.gate_up_swiglu(x, copies[i % len(copies)], sw, tiled=True)
     torch.cuda.synchronize()
     print("pmc driver done", flush=True)
+
+
+def read_probe(torch, fp8, synthetic, quantize_rows) -> dict:
+    """The decode ceiling at M = 16: for every decode shape (the six
+    projections, the merged q/k/v and the 9B model's merged widths), the GEMM
+    kernel's time next to the time a pure streaming read of the same codes
+    takes (tests/csrc/read_probe.hip: each wave issues all its 1 KB loads at
+    once, then folds them into one stored word), in the GEMM's own launch
+    shape (workgroups and threads from jv_fp8_launch_shape) and in the fastest
+    of a sweep of shapes (256 or 512 threads, 4-32 KB per wave). Same harness
+    as the GEMM lines: graphs of back-to-back launches over weight copies
+    rotated through >= 512 MB."""
+    import ctypes
+
+    from jeeves_amd import _lib, device
+
+    hooks_path = ROOT / "tests" / "libjeeves_fp8_testhooks.so"
+    if not hooks_path.exists():
+        raise RuntimeError("the read probe is in the test-hook library: run `python -m jeeves_amd.build --tests`")
+    hooks = ctypes.CDLL(str(hooks_path))
+    probe = hooks.th_read_probe
+    probe.restype = ctypes.c_int
+    probe.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                      ctypes.c_void_p]
+    b = Bench(torch)
+    M = 16
+    cus = device.sm_count(torch.device("cuda", 0))
+    weights = make_weights(torch, synthetic, quantize_rows)
+    weights.update(merged_9b_weights(torch, synthetic, quantize_rows))
+    rot = Rotation(weights)
+    shapes = dict(synthetic.SHAPES, qkv=layer_shapes(synthetic)["qkv"],
+                  **{name: (N, synthetic.HIDDEN) for name, N in MERGED_9B.items()})
+    sink = torch.empty(1 << 20, dtype=torch.int32, device="cuda")
+    out = {}
+    for name, (N, K) in shapes.items():
+        nbytes = N * K
+        x = synthetic.decode_case(name if name in synthetic.SHAPES else "q", M)[0].cuda()
+        gemm_ms = kernel_ms(b, fp8, rot.copies(name), quantized_operands(torch, fp8, x), 40)
+        shape = (ctypes.c_int32 * 4)()
+        _lib.check(_lib.lib().jv_fp8_launch_shape(M, N, K, cus, shape))
+        wg, threads = shape[1], shape[2]
+
+        def probe_ms(wg_, threads_, lpw):
+            def launch(wq, sw):
+                rc = probe(wq.data_ptr(), nbytes, wg_, threads_, lpw, sink.data_ptr(), torch.cuda.current_stream().cuda_stream)
+                if rc:
+                    raise RuntimeError(f"read probe refused {wg_} x {threads_} x {lpw} KB for {nbytes} bytes")
+            return launches_ms(b, rot.copies(name), launch, 40)
+
+        per_wave = nbytes / (wg * (threads // 64) * 1024)
+        in_shape = None
+        if per_wave == int(per_wave) and int(per_wave) in (4, 8, 16, 24, 32):
+            in_shape = {"us": round(probe_ms(wg, threads, int(per_wave)) * 1e3, 2),
+                        "shape": [wg, threads, int(per_wave)]}
+        best = None
+        for threads_ in (256, 512):
+            for lpw in (4, 8, 16, 32):
+                wg_ = nbytes // ((threads_ // 64) * lpw * 1024)
+                if wg_ * (threads_ // 64) * lpw * 1024 != nbytes or wg_ * (threads_ // 64) > (1 << 20):
+                    continue
+                us = probe_ms(wg_, threads_, lpw) * 1e3
+                if best is None or us < best["us"]:
+                    best = {"us": round(us, 2), "shape": [wg_, threads_, lpw]}
+        out[name] = {"N": N, "K": K, "code_bytes": nbytes,
+                     "gemm": dict(rate(M, N, K, gemm_ms, "hbm"), shape=[wg, threads]),
+                     "read_in_gemm_shape": in_shape, "read_fastest": best}
+        log(f"bench: read probe {name}: {out[name]}")
+    rot.drop()
+    return {"note": "M=16 decode GEMM vs a pure streaming read of its codes; shapes are [workgroups, threads, "
+                    "KB per wave] for reads and [workgroups, threads] for the GEMM; every time includes its launch",
+            "shapes": out}
 
 
 def device_weight(torch, synthetic, N: int, K: int, seed: int):
@@ -570,6 +724,8 @@ def main() -> int:
                     help="skip the decoder-layer (LoRA, M=512), 32-layer ragged-mix and lm_head measurements")
     ap.add_argument("--pmc-driver", action="store_true",
                     help="run only the hardware-counter workload (copy calibration + gate+up GEMMs), no timing")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="run only the decode ceiling table: each M=16 decode GEMM vs a pure read of its codes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the FP8 linear path on one GPU; runs on more than one GPU are not part of this build",
@@ -586,6 +742,9 @@ def main() -> int:
         return 2
     if args.pmc_driver:
         pmc_driver(torch, fp8, synthetic, quantize_rows)
+        return 0
+    if args.read_probe:
+        print(json.dumps(read_probe(torch, fp8, synthetic, quantize_rows)), flush=True)
         return 0
     b = Bench(torch)
     dev_name = torch.cuda.get_device_name(0)
@@ -618,10 +777,28 @@ def main() -> int:
         merged = per_kernel(b, torch, fp8, synthetic, rot, M, synthetic.decode_case, 40, "hbm", merged_shapes)
         log(f"bench: 9B merged projections {merged}")
     sweep = {}
+    rowmajor, w8a16, mlp = {}, {}, {}
     if not args.no_sweep:
         for m in DECODE_SWEEP_ROWS:
             sweep[f"m{m}"] = per_kernel(b, torch, fp8, synthetic, rot, m, synthetic.decode_case, 16, "hbm")
         log(f"bench: decode sweep done ({', '.join(sweep)})")
+        for m in (16, 64):
+            mlp[f"m{m}"] = mlp_steps(b, torch, fp8, synthetic, weights, m, 40)
+        log(f"bench: MLP block, reference-shaped vs fused {mlp}")
+        # the single-copy layout (FP8Linear.TILED_COPY = False): the kernels read the row-major codes
+        rot_rm = Rotation({name: (fp8.untile_weight(weights[name][0]), weights[name][1])
+                           for name in (*synthetic.SHAPES, "qkv")})
+        for m in (16, 64):
+            rowmajor[f"m{m}"] = per_kernel(b, torch, fp8, synthetic, rot_rm, m, synthetic.decode_case, 16, "hbm",
+                                           tiled=False)
+        rot_rm.drop()
+        del rot_rm
+        torch.cuda.empty_cache()
+        log(f"bench: row-major weights {rowmajor}")
+        for m in W8A16_ROWS:
+            case = synthetic.decode_case if m <= 64 else synthetic.prefill_case
+            w8a16[f"m{m}"] = per_kernel_w8a16(b, torch, fp8, synthetic, rot, m, case, 16 if m <= 64 else 4)
+        log(f"bench: W8A16 parity mode {w8a16}")
 
     result = {
         "metric": METRIC,
@@ -637,10 +814,12 @@ def main() -> int:
         "dtype": "fp8_e4m3 (fp32 accumulate)",
         "data": "synthetic (seeded random-init weights and activations)",
         "config": {
-            "workload": f"decode M={M}: one 9B-class decoder layer's FP8 linears as the reference engine runs them: "
-                        f"q/k/v merged 4096->6144, o 4096->4096, gate+up 4096->24576 with SwiGLU in its GEMM "
-                        f"epilogue, down 12288->4096; each distinct input quantized once (4 quantizer + 4 GEMM "
-                        f"launches), HIP graph replay, weights in FP8Linear's tiled layout rotated over {n_sets} copies",
+            "workload": f"decode M={M}: one 9B-class decoder layer's FP8 linears with q/k/v merged as the engine "
+                        f"merges them (4096->6144), o 4096->4096, and the MLP as FP8SwiGLU runs it after "
+                        f"fuse_swiglus: gate+up 4096->24576 as one GEMM with SwiGLU in its epilogue, the "
+                        f"quantization of h, down 12288->4096 (the reference-shaped MLP is decode.mlp_m16); each "
+                        f"distinct input quantized once (4 quantizer + 4 GEMM launches), HIP graph replay, weights "
+                        f"in FP8Linear's tiled layout rotated over {n_sets} copies",
             "tokens": M,
             "device": dev_name,
         },
@@ -659,7 +838,15 @@ def main() -> int:
             "kernels_m16": kernels,
             "kernels_m16_9b_merged": merged,
             "kernels_sweep": sweep,
+            "mlp": dict(mlp, note="the MLP block at decode sizes: reference_shaped = gate and up as two FP8Linear "
+                                  "calls, torch's F.silu(gate) * up, down (model/model.py:581-584 after the import "
+                                  "swap alone); fused = FP8SwiGLU after fuse_swiglus"),
+            "kernels_rowmajor": dict(rowmajor, note="GEMM kernels on the row-major codes (FP8Linear.TILED_COPY = "
+                                                    "False: one copy of the codes in HBM), same harness as "
+                                                    "kernels_m16 / kernels_sweep"),
         },
+        "w8a16": dict(w8a16, note="W8A16 parity mode (fp8_matmul_w8a16, the reference's arithmetic): GB/s vs "
+                                  "8 TB/s at M <= 64, TFLOP/s vs the dense bf16 MFMA peak 2.5 PFLOP/s at M = 2048"),
     }
 
     if not args.no_prefill:

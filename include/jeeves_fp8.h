@@ -188,7 +188,10 @@ int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_
  * and 16 channels of h, the largest |h| as a bf16 magnitude pattern (NaN
  * sorts above inf). I a positive multiple of 16, K <= 16384. workspace:
  * jv_fp8_linear_workspace_bytes(M, 2I, K, rank) bytes suffice; the fused
- * GEMM never splits K. The gate+up output [M, 2I] never reaches memory. */
+ * GEMM never splits K. The gate+up output [M, 2I] never reaches memory.
+ * h follows the reference's F.silu(gate) * up branch (two bf16 roundings);
+ * its fla branch (_fla_swiglu, one rounding) is not matched, and parity with
+ * it is unpinned. */
 int jv_fp8_linear_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
                          const void* lora_a, const void* lora_b, int64_t lora_rank, float lora_scaling, void* h,
                          int64_t ldh, uint16_t* h_amax, int64_t M, int64_t I, int64_t K, void* workspace,
@@ -233,6 +236,13 @@ int jv_fp8_untile_weight(const void* tiled, int64_t N, int64_t K, void* codes, i
  * inference/fp8.py:118-123), and the tile counters it needs. */
 int jv_fp8_split_for(int64_t M, int64_t N, int64_t K, int cu_count);
 int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count);
+
+/* The same introspection for the whole launch: shape[0] = the GEMM kernel
+ * (0 decode, 1 prefill lockstep tiles, 2 prefill ping-pong tiles), shape[1] =
+ * its workgroups (K splits included), shape[2] = threads per workgroup,
+ * shape[3] = K splits across workgroups. For measurement tools that
+ * compare a GEMM with other launches of its shape. */
+int jv_fp8_launch_shape(int64_t M, int64_t N, int64_t K, int cu_count, int32_t* shape);
 
 #ifdef __cplusplus
 }

@@ -47,6 +47,7 @@ SIGNATURES: dict[str, tuple] = {
     "jv_fp8_untile_weight": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p]),
     "jv_fp8_split_for": (c_int, [c_int64, c_int64, c_int64, c_int]),
     "jv_fp8_counters_needed": (c_int64, [c_int64, c_int64, c_int64, c_int]),
+    "jv_fp8_launch_shape": (c_int, [c_int64, c_int64, c_int64, c_int, POINTER(c_int32)]),
 }
 
 _lib = None

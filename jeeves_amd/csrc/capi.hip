@@ -157,15 +157,13 @@ static __device__ __align__(256) uint8_t scratch[JV_FP8_NOALLOC_SCRATCH_BYTES];
 std::mutex g_scratch_mu;
 std::atomic<uint8_t*> g_scratch[kMaxDevices];
 
-__global__ void zero_words(int32_t* p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
-
-// The calling thread's current device's scratch address; on the first call on
-// a device, also clears its tile counters (a fill kernel on `stream`, which
-// orders it before the GEMM that follows on the same stream).
-int scratch_of_current_device(hipStream_t stream, uint8_t** out) {
+// The calling thread's current device's scratch address. The tile counters at
+// its start are zero without a clear: a __device__ array without initializer
+// is zero-filled when the code object is loaded onto the device (static
+// storage), and every kernel that counts in leaves its counters at zero. So the
+// first call puts nothing on `stream` beyond its own launches, and may itself
+// be captured into a graph.
+int scratch_of_current_device(uint8_t** out) {
   int device = -1;
   if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices)
     return fail(JV_ERR_HIP, "cannot query the current HIP device");
@@ -177,9 +175,6 @@ int scratch_of_current_device(hipStream_t stream, uint8_t** out) {
       if (int rc = hip_status(hipGetSymbolAddress(reinterpret_cast<void**>(&p), HIP_SYMBOL(scratch)),
                               "no-allocation scratch address"))
         return rc;
-      zero_words<<<dim3((unsigned)(kNoAllocCounterSlots / 256)), dim3(256), 0, stream>>>(reinterpret_cast<int32_t*>(p),
-                                                                                     (int)kNoAllocCounterSlots);
-      if (int rc = hip_status(hipGetLastError(), "no-allocation scratch clear")) return rc;
       g_scratch[device].store(p, std::memory_order_release);
     }
   }
@@ -377,6 +372,27 @@ int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count) {
   return p.splits > 1 ? p.groups : 0;
 }
 
+int jv_fp8_launch_shape(int64_t M, int64_t N, int64_t K, int cu_count, int32_t* shape) {
+  if (!shape) return fail(JV_ERR_VALUE, "shape needs 4 slots");
+  if (int rc = check_gemm_shape(M, N, K)) return rc;
+  if (M <= 0 || cu_count <= 0) return fail(JV_ERR_VALUE, "launch shape needs M > 0 and a CU count");
+  if (jv::decode_kernel_for(M, N, cu_count)) {
+    const jv::DecodePlan p = jv::decode_plan(M, N, K, cu_count);
+    shape[0] = 0;
+    shape[1] = p.groups * p.splits;
+    shape[2] = 64 * p.waves;
+    shape[3] = p.splits;
+    return JV_OK;
+  }
+  const jv::PrefillTile t = jv::prefill_tile(M, N, K, cu_count);
+  const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+  shape[0] = t.pingpong ? 2 : 1;
+  shape[1] = (int32_t)(tiles * t.splits);
+  shape[2] = t.pingpong ? 512 : 64 * t.wgm * t.wgn;
+  shape[3] = t.splits;
+  return JV_OK;
+}
+
 int jv_fp8_linear_noalloc(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
                           const void* lora_a, const void* lora_b, int64_t lora_rank, float lora_scaling, void* y,
                           int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
@@ -391,7 +407,7 @@ int jv_fp8_linear_noalloc(const void* x, int64_t ldx, const void* w, int64_t ldw
                 "jv_fp8_linear with a workspace instead",
                 (long long)M, (long long)N, (long long)K, (long long)need, (long long)kNoAllocWorkspaceBytes);
   uint8_t* base = nullptr;
-  if (int rc = scratch_of_current_device((hipStream_t)stream, &base)) return rc;
+  if (int rc = scratch_of_current_device(&base)) return rc;
   return jv_fp8_linear(x, ldx, w, ldw, w_scale, bias, lora_a, lora_b, lora_rank, lora_scaling, y, ldy, M, N, K,
                        base + kNoAllocCounterBytes, kNoAllocWorkspaceBytes, reinterpret_cast<int32_t*>(base),
                        kNoAllocCounterSlots, stream);
@@ -408,8 +424,10 @@ int jv_fp8_linear_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw,
   if (!packed_codes(K)) return fail(JV_ERR_VALUE, "the fused SwiGLU needs in_features <= 16384, got %lld", (long long)K);
   if (M == 0) return JV_OK;
   if (!aligned16(x) || (ldx * 2) % 16) return fail(JV_ERR_VALUE, "the fp8 GEMM needs 16-byte aligned operand rows");
-  if (ldh < I || !h || (h_amax && (reinterpret_cast<uintptr_t>(h_amax) & 1)))
-    return fail(JV_ERR_VALUE, "h needs a row stride of at least %lld", (long long)I);
+  if (!h || ldh < I) return fail(JV_ERR_VALUE, "h needs a row stride of at least %lld", (long long)I);
+  if (!aligned16(h) || (ldh * 2) % 16) return fail(JV_ERR_VALUE, "h needs 16-byte aligned rows");
+  if (h_amax && (reinterpret_cast<uintptr_t>(h_amax) & 1))
+    return fail(JV_ERR_VALUE, "h_amax must be 2-byte aligned (uint16 maxima)");
   if (int rc = check_weight(2 * I, K, ldw, w)) return rc;
   const int64_t need = round_up(codes_bytes(M, K), 256) + round_up(M * 4, 256) + round_up(M * lora_rank * 4, 256);
   if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255))

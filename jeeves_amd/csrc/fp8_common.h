@@ -61,7 +61,11 @@ __device__ __forceinline__ float silu_of_bf16(float g) {
 
 // SwiGLU on bf16 values (SwiGLU.forward, model/model.py:583, as torch runs it
 // on bf16 tensors): silu(g) rounded to bf16, times up (exact in fp32), rounded
-// to bf16.
+// to bf16. This is the reference's F.silu(gate) * up branch; its fla branch
+// (_fla_swiglu, taken where flash-linear-attention is installed) rounds only
+// the product, and parity with it is unpinned. Every kernel's SwiGLU rounding
+// goes through this function or swiglu_pair_f32 below, so a single-rounding
+// variant would replace these two alone.
 __device__ __forceinline__ uint32_t swiglu_bf16(uint32_t g16, uint32_t u16) {
   const float sb = bf16_to_f32(f32_to_bf16(silu_of_bf16(bf16_to_f32(g16))));
   return f32_to_bf16(sb * bf16_to_f32(u16));

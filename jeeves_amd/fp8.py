@@ -383,7 +383,10 @@ def gate_up_swiglu(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *
     up rows (the fused gate+up linear), ``scale``/``bias`` [2I], LoRA B
     [2I, r]. Returns h bf16 [M, I], bitwise ``swiglu(fp8_matmul(x, ...))`` of
     the two halves; with ``amax`` also the per-token largest |h| over each
-    16 channels (uint16 bf16 magnitude patterns [M, I/16])."""
+    16 channels (uint16 bf16 magnitude patterns [M, I/16]). h is the
+    reference's ``F.silu(gate) * up`` branch on bf16 (silu rounded, then the
+    product); its fla branch (``_fla_swiglu``, one rounding) is not matched and
+    parity with it is unpinned."""
     M, K = x.shape
     N = weight.shape[0]
     _check_weight(K, weight)
@@ -504,12 +507,19 @@ class FP8Linear(nn.Module):
             module.kernel_weight()
 
     def _weight_key(self) -> tuple[int, int]:
-        return self.weight.data_ptr(), self.weight._version
+        # Inference tensors (made under torch.inference_mode) keep no version
+        # counter: their key is the address alone, and in-place writes to them
+        # need retile().
+        w = self.weight
+        return w.data_ptr(), (-1 if torch.is_inference(w) else w._version)
 
     def kernel_weight(self) -> tuple[torch.Tensor, bool]:
         """The codes the kernels read and whether they are tiled: the tiled
         copy, rebuilt first if ``weight`` changed since it was made, or
-        ``weight`` itself."""
+        ``weight`` itself. A change is a new ``weight`` tensor or an in-place
+        write that bumps its version counter (``copy_``, ``load_state_dict``);
+        writes that bypass the counter (through ``weight.data``, or into an
+        inference tensor) must be followed by ``retile()``."""
         if not self.tiled:
             return self.weight, False
         key = self._weight_key()
@@ -517,6 +527,14 @@ class FP8Linear(nn.Module):
             _tile_into(self.weight, self.tiled_codes)
             self._tiled_from = key
         return self.tiled_codes, True
+
+    @torch.no_grad()
+    def retile(self) -> None:
+        """Rebuild the tiled copy from ``weight`` now (after writes the
+        version counter does not see)."""
+        if self.tiled:
+            self._tiled_from = None
+            self.kernel_weight()
 
     def codes(self) -> torch.Tensor:
         """The e4m3 codes, row-major [N, K] (``weight``)."""
@@ -587,13 +605,62 @@ class FP8SwiGLU(nn.Module):
     and up projections as one FP8 GEMM (``gate_up``: gate rows first, then up
     rows) whose epilogue applies SwiGLU and writes h, the down projection's
     quantization of h, then the down GEMM. The gate+up output never reaches
-    memory; the result is bitwise that of the separate steps."""
+    memory; the result is bitwise that of the separate steps.
 
-    def __init__(self, gate_up: FP8Linear, down: FP8Linear):
+    h is ``F.silu(gate) * up`` on bf16 tensors (silu rounded to bf16, then the
+    product rounded), the reference's own expression where its fused
+    ``_fla_swiglu`` is not in use (``model/model.py:583``). fla's kernel rounds
+    once; flash-linear-attention is not installed here and no fixture holds its
+    outputs, so parity with that branch is unpinned.
+
+    Built with ``parts`` (``from_mlp``/``fuse_swiglus``), the module keeps the
+    reference's attribute and state-dict names: ``gate_proj``, ``up_proj`` and
+    ``down_proj`` are its submodules (the first two views of the merged
+    ``gate_up``, as ``FP8Linear.concatenated`` makes them), and ``gate_up`` is
+    held outside the module tree, as the engine's merged projections are
+    (``inference/engine.py:154-165``). Build it after the weights are on their
+    device: moving the module afterwards would break the views."""
+
+    def __init__(self, gate_up: FP8Linear, down: FP8Linear, parts: tuple[FP8Linear, FP8Linear] | None = None):
         super().__init__()
         if gate_up.out_features != 2 * down.in_features:
             raise ValueError("gate_up must have twice down's in_features outputs")
-        self.gate_up, self.down = gate_up, down
+        if parts is None:
+            self.gate_up, self.down = gate_up, down
+        else:
+            self.gate_proj, self.up_proj, self.down_proj = parts[0], parts[1], down
+            object.__setattr__(self, "gate_up", gate_up)
+            object.__setattr__(self, "down", down)
+
+    @classmethod
+    def from_mlp(cls, mlp: nn.Module) -> "FP8SwiGLU":
+        """The fused form of a module shaped like the reference's ``SwiGLU``
+        (``gate_proj``, ``up_proj``, ``down_proj`` as ``FP8Linear``s, e.g. after
+        ``replace_linears``): gate and up merged with ``FP8Linear.concatenated``
+        (gate rows, then up rows), so both become views of the merged codes."""
+        gate, up, down = mlp.gate_proj, mlp.up_proj, mlp.down_proj
+        if not all(isinstance(m, FP8Linear) for m in (gate, up, down)):
+            raise ValueError("gate_proj, up_proj and down_proj must be FP8Linear modules")
+        if gate.in_features != up.in_features or gate.out_features != up.out_features or \
+                gate.out_features != down.in_features:
+            raise ValueError(f"gate {gate.out_features}x{gate.in_features}, up {up.out_features}x{up.in_features} and "
+                             f"down {down.out_features}x{down.in_features} do not form a SwiGLU block")
+        if gate.lora is not None or up.lora is not None:
+            raise ValueError("gate_proj and up_proj carry their own LoRA adapters; the merged gate+up GEMM takes one")
+        if (gate.bias is None) != (up.bias is None):
+            raise ValueError("gate_proj and up_proj must both have a bias or neither")
+        merged = FP8Linear.concatenated([gate, up])
+        if gate.bias is not None:
+            # One bias buffer as for the codes: the parts' biases become views of it.
+            merged.bias = nn.Parameter(torch.cat([gate.bias, up.bias]), requires_grad=False)
+            gate.bias, up.bias = (nn.Parameter(b, requires_grad=False) for b in merged.bias.split(gate.out_features))
+        merged.activations = gate.activations
+        return cls(merged, down, parts=(gate, up))
+
+    def set_activations(self, mode: str) -> None:
+        """``FP8Linear.set_activations`` on every projection of the block."""
+        for m in {id(m): m for m in (self.gate_up, self.down, *self.children())}.values():
+            m.set_activations(mode)
 
     def fused(self) -> bool:
         """Whether the gate+up GEMM applies SwiGLU in its epilogue (the
@@ -634,6 +701,30 @@ class FP8SwiGLU(nn.Module):
                                  lora_scaling=self.down.lora[2] if lora_a is not None else 0.0,
                                  packed_rows=M if packed else None, tiled=tiled)
         return y.view(*shape[:-1], self.down.out_features)
+
+
+def _swiglu_block(m: nn.Module) -> bool:
+    return not isinstance(m, FP8SwiGLU) and all(isinstance(getattr(m, name, None), FP8Linear)
+                                                for name in ("gate_proj", "up_proj", "down_proj"))
+
+
+def fuse_swiglus(module: nn.Module) -> int:
+    """Swap every SwiGLU block under ``module`` (a child with ``FP8Linear``
+    ``gate_proj``, ``up_proj`` and ``down_proj``, the reference's ``SwiGLU``
+    after ``replace_linears``, ``model/model.py:574-584``) for
+    ``FP8SwiGLU.from_mlp`` of it, in place, the way the engine merges
+    projections that read the same input (``inference/engine.py:154-165``).
+    Blocks whose gate or up carries its own LoRA adapter stay as they are.
+    Returns the number of blocks fused."""
+    n = 0
+    for name, child in module.named_children():
+        if _swiglu_block(child):
+            if child.gate_proj.lora is None and child.up_proj.lora is None:
+                setattr(module, name, FP8SwiGLU.from_mlp(child))
+                n += 1
+        else:
+            n += fuse_swiglus(child)
+    return n
 
 
 def load_view(model: str, drafter: str, block: int, device: torch.device):

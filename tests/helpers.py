@@ -91,6 +91,72 @@ EQUAL_MIN = 0.97           # share bitwise equal to the exact result rounded to 
 BOUND_MAGNITUDE = 2.0 ** -11  # |out-exact| <= |exact| 2^-8 + magnitude * this
 
 
+def gemm_magnitude(xq, sx, wq, sw) -> np.ndarray:
+    """sum_k |x[m,k] w[n,k]| of the dequantized FP8 operands (float64)."""
+    xd = np.abs(oracle.e4m3_decode(xq).astype(np.float64) * np.asarray(sx, np.float64)[:, None])
+    wd = np.abs(oracle.e4m3_decode(wq).astype(np.float64) * np.asarray(sw, np.float64)[:, None])
+    return xd @ wd.T
+
+
+def gemm_allowance(exact: np.ndarray, magnitude: np.ndarray) -> np.ndarray:
+    """Largest |out - exact| the GEMM criteria accept for a bf16 output without
+    a bias: |exact| 2^-8 + magnitude * BOUND_MAGNITUDE."""
+    return np.abs(exact) * 2.0 ** -8 + magnitude * BOUND_MAGNITUDE
+
+
+def _silu_range(lo: np.ndarray, hi: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Range of silu(g) = g / (1 + e^-g) over [lo, hi] (float64): increasing
+    above its minimum at g0 = -1.27846..., decreasing below it."""
+    g0, s0 = -1.2784645427610738, -0.2784645427610738
+
+    def silu(g):
+        with np.errstate(over="ignore"):
+            return g / (1.0 + np.exp(-g))
+
+    a, b = silu(lo), silu(hi)
+    low = np.where((lo <= g0) & (g0 <= hi), s0, np.minimum(a, b))
+    return low, np.maximum(a, b)
+
+
+def swiglu_criteria(h_bits: np.ndarray, xq, sx, wq, sw, bias_bits=None) -> dict:
+    """The acceptance numbers for h = SwiGLU of a fused gate+up GEMM (weight
+    rows: gate, then up), against the oracle alone:
+    * equal: share of h bitwise equal to ``oracle.swiglu_bf16`` of the exact
+      gate and up products rounded once to bf16 (with a bias, plus the bias in
+      bf16 as the unfused path adds it), i.e. ``F.silu(gate) * up`` on the
+      exact-rounded GEMM outputs (``model/model.py:583``);
+    * bound: h inside the interval SwiGLU maps the GEMM criteria's per-output
+      allowance to: gate g and up u each within ``gemm_allowance`` of their
+      exact values (a bias adds its bf16 rounding), silu's range over g's
+      interval, one bf16 rounding of silu (2^-8 relative), the product's range
+      over the box, and one bf16 rounding of the product."""
+    wq = np.asarray(wq)
+    I = wq.shape[0] // 2
+    exact = oracle.gemm_exact_f64(xq, sx, wq, sw)
+    allow = gemm_allowance(exact, gemm_magnitude(xq, sx, wq, sw))
+    g_bits, u_bits = oracle.f64_to_bf16(exact[:, :I]), oracle.f64_to_bf16(exact[:, I:])
+    lo, hi = exact - allow, exact + allow
+    if bias_bits is not None:
+        bias_bits = np.asarray(bias_bits, np.uint16)
+        g_bits = oracle.add_bias_bf16(g_bits, bias_bits[:I])
+        u_bits = oracle.add_bias_bf16(u_bits, bias_bits[I:])
+        b = oracle.bf16_to_f32(bias_bits).astype(np.float64)[None, :]
+        lo, hi = lo + b, hi + b
+        lo, hi = lo - np.abs(lo) * 2.0 ** -8, hi + np.abs(hi) * 2.0 ** -8
+    want = oracle.swiglu_bf16(g_bits, u_bits)
+    s_lo, s_hi = _silu_range(lo[:, :I], hi[:, :I])
+    s_lo, s_hi = s_lo - np.abs(s_lo) * 2.0 ** -8, s_hi + np.abs(s_hi) * 2.0 ** -8
+    u_lo, u_hi = lo[:, I:], hi[:, I:]
+    corners = np.stack([s_lo * u_lo, s_lo * u_hi, s_hi * u_lo, s_hi * u_hi])
+    p_lo, p_hi = corners.min(axis=0), corners.max(axis=0)
+    p_lo, p_hi = p_lo - np.abs(p_lo) * 2.0 ** -8, p_hi + np.abs(p_hi) * 2.0 ** -8
+    h = oracle.bf16_to_f32(np.asarray(h_bits, np.uint16)).astype(np.float64)
+    finite = np.isfinite(exact[:, :I]) & np.isfinite(exact[:, I:])
+    inside = (p_lo <= h) & (h <= p_hi)
+    return {"equal": oracle.bitwise_equal_fraction(h_bits, want), "bound": bool(inside[finite].all()),
+            "outside": int((~inside & finite).sum()), "want_bits": want}
+
+
 def gemm_criteria(out_bits: np.ndarray, xq, sx, wq, sw, bias_bits=None, lora_term=None) -> dict:
     """The acceptance numbers for one GEMM output:
     * equal: share bitwise equal to the exact result rounded once to bf16

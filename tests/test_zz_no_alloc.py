@@ -52,6 +52,31 @@ def without_workspace(x, w, ldw, sw, bias, lora, N):
     return y
 
 
+def test_first_noalloc_call_captured_in_a_graph():
+    """The first call of the no-allocation entry point in this process (this
+    test comes first in the file, and nothing else calls it) made inside a
+    captured graph: the graph holds only the call's own launches (the scratch's
+    tile counters are zero from the code object's load, with no clear on the
+    stream), and every replay -- with eager work and a new input between
+    replays -- equals the workspace entry point on the split-K decode path,
+    whose tile counters live in the scratch."""
+    N, K, M = 256, 4096, 16
+    wq, sw = quantize_rows(synthetic.weight(N, K, 7000).cuda())
+    w = wq.view(torch.uint8)
+    x = synthetic.activations_outliers(M, K, 7001).cuda()
+    assert _lib.lib().jv_fp8_split_for(M, N, K, torch.cuda.get_device_properties(0).multi_processor_count) > 1
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = without_workspace(x, w, K, sw, None, None, N)
+    for rep in range(4):
+        x.copy_(synthetic.activations_outliers(M, K, 7002 + rep).cuda())
+        want = with_workspace(x, w, K, sw, None, None, N)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), rep
+
+
 # (N, K, first M, second M, tiled, bias, lora): split-K decode, plain decode,
 # 64x64 prefill tiles on a wide weight, split-K 64x64 prefill tiles (4
 # splits), split-K 128x128 prefill tiles (2 and 4 splits, 16 MiB of
