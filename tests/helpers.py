@@ -4,6 +4,7 @@ the test-hook library, and the acceptance checks of the reference's tests."""
 from __future__ import annotations
 
 import ctypes
+import math
 from ctypes import c_float, c_int, c_int64, c_uint32, c_void_p
 from pathlib import Path
 
@@ -80,15 +81,39 @@ def stream() -> int:
 
 
 # Tolerances of the FP8 x FP8 GEMM against the exact product of the same FP8
-# inputs. gfx950's FP8 MFMA adds each group of 8 products aligned to the
-# group's largest with a ~13-bit window (products more than 2^-13 below it are
-# truncated; the accumulator input is added exactly), which gives ~1e-4
-# relative error on realistic data: ~1-2% of outputs round to the bf16
-# neighbour of the exact result. The reference's 99.5% criterion
-# (inference/cuda_test.py:90) is for its fp16 MMA, which sums in fp32.
+# inputs. gfx950's FP8 MFMA adds the products of each aligned run of 8 k with
+# the bits below 2^-13 of the run's largest product dropped (the accumulator
+# input is added exactly), which gives ~1e-4 relative error on realistic data:
+# ~1-2% of outputs round to the bf16 neighbour of the exact result. The
+# reference's 99.5% criterion (inference/cuda_test.py:90) is for its fp16 MMA,
+# which sums in fp32.
 REL_L2_MAX = 1e-3          # bf16 output vs bf16 dequantize-then-matmul
-EQUAL_MIN = 0.97           # share bitwise equal to the exact result rounded to bf16
-BOUND_MAGNITUDE = 2.0 ** -11  # |out-exact| <= |exact| 2^-8 + magnitude * this
+# Share of outputs bitwise equal to the exact result rounded to bf16, per
+# input family (measured: 0.977-0.989 per call on outlier and heavy-tail
+# workloads, 0.984-0.994 per call and 0.991 pooled on the reference's
+# acceptance inputs). Each call is held to equal_floor(n, bar): the bar less
+# three binomial standard deviations for its n outputs.
+EQUAL_MIN = 0.98            # outlier and heavy-tail workloads, per call
+EQUAL_MIN_REFERENCE = 0.99  # inference/cuda_test.py:79-85 inputs, pooled over the nine row counts of a weight
+# SwiGLU outputs h as activations (the down projection): h = silu(g) u is a
+# product of two roughly Gaussian values, so its rows quantize to more small
+# codes and more products lose bits in the alignment window (measured
+# 0.9736-0.9743 per call).
+EQUAL_MIN_SWIGLU_H = 0.97
+# |out - exact| <= |exact| 2^-8 + magnitude * BOUND_MAGNITUDE. The window
+# drops less than 7 * 2^-13 of each run's largest product (worst case
+# 7 * 2^-13 * G, G = sum over runs of the largest |product|, G/magnitude
+# about 0.4 on these inputs: 2^-11.4 * magnitude); the dropped bits carry
+# the products' mixed signs, and the largest error measured beyond
+# |exact| 2^-8 is 2^-13.3 * magnitude.
+BOUND_MAGNITUDE = 2.0 ** -12
+
+
+def equal_floor(n: int, bar: float) -> float:
+    """Least equal share a call with n outputs may show when its true share is
+    at least `bar`: the bar less three binomial standard deviations (0.9792
+    for 2^18 outputs at bar 0.98, 0.967 for 1024)."""
+    return bar - 3.0 * math.sqrt(bar * (1.0 - bar) / n) if n else 0.0
 
 
 def gemm_magnitude(xq, sx, wq, sw) -> np.ndarray:
@@ -191,6 +216,7 @@ def gemm_criteria(out_bits: np.ndarray, xq, sx, wq, sw, bias_bits=None, lora_ter
     exact_rounded = oracle.bf16_to_f32(exact_bits).astype(np.float64)
     bound_mag = magnitude * (BOUND_MAGNITUDE / 2.0 ** -20) + slack * 2.0 ** 20
     return {
+        "n": int(np.asarray(out_bits).size),
         "equal": oracle.bitwise_equal_fraction(out_bits, exact_bits),
         "rel_l2": oracle.rel_l2(out[finite], exact_rounded[finite]) if finite.any() else 0.0,
         "bound": oracle.within_metal_bound(out[finite], exact[finite], bound_mag[finite]) if finite.any() else True,

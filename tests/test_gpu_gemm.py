@@ -3,9 +3,10 @@ with the oracle, under the reference's own acceptance criteria
 (inference/cuda_test.py:74-94, model/metal_test.py:202-243):
 rel-L2 <= 1e-3 against the bf16 dequantize-then-matmul output on the same FP8
 inputs, outputs bitwise equal to the exact result rounded once to bf16 (at
-least 97%: the FP8 MFMA's in-instruction alignment moves ~1-2% of outputs to
-the neighbouring bf16 value, where the reference's fp16 MMA gets 99.5%), the
-float64 error bound |out - exact| <= |exact| 2^-8 + magnitude 2^-11 (the form
+least 98% per call, less three binomial standard deviations for the call's
+output count: the FP8 MFMA's in-instruction alignment moves ~1-2% of outputs
+to the neighbouring bf16 value, where the reference's fp16 MMA gets 99.5%), the
+float64 error bound |out - exact| <= |exact| 2^-8 + magnitude 2^-12 (the form
 of model/metal_test.py:219-221), finite outputs, and bitwise-identical repeat
 calls. The tolerances live in tests/helpers.py."""
 
@@ -36,7 +37,7 @@ def check(y: torch.Tensor, x: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor, 
     c = helpers.gemm_criteria(helpers.bits(y), xq, sx, helpers.codes_np(wq), sw.cpu().numpy(),
                               bias_bits=helpers.bits(bias) if bias is not None else None, lora_term=lora_term)
     assert c["finite_match"], ("non-finite outputs where the exact result is finite (or the reverse)", c)
-    assert c["equal"] >= equal_min, c
+    assert c["equal"] >= helpers.equal_floor(c["n"], equal_min), c
     assert c["rel_l2"] <= REL_L2_MAX, c
     assert c["bound"], c
     return c
@@ -480,4 +481,4 @@ def test_swiglu_packed_codes_feed_down_projection(M):
     y_row = fp8_matmul_quantized(codes, scales, wq, sw)
     y_packed = fp8_matmul_quantized(pcodes, pscales, wq, sw, packed_rows=M)
     assert torch.equal(y_row, y_packed)
-    check(y_packed, h, wq, sw)
+    check(y_packed, h, wq, sw, equal_min=helpers.EQUAL_MIN_SWIGLU_H)

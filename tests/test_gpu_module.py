@@ -131,4 +131,5 @@ def test_decoder_layer_stack_with_lora():
         got = oracle.bf16_to_f32(helpers.bits(y)).astype(np.float64)
         exact_bits = oracle.f64_to_bf16(exact)
         assert oracle.rel_l2(got, oracle.bf16_to_f32(exact_bits)) <= helpers.REL_L2_MAX, name
-        assert oracle.bitwise_equal_fraction(helpers.bits(y), exact_bits) >= helpers.EQUAL_MIN, name
+        bar = helpers.EQUAL_MIN_SWIGLU_H if name == "down" else helpers.EQUAL_MIN
+        assert oracle.bitwise_equal_fraction(helpers.bits(y), exact_bits) >= helpers.equal_floor(y.numel(), bar), name

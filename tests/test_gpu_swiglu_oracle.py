@@ -30,11 +30,13 @@ from tests import helpers
 
 pytestmark = pytest.mark.gpu
 
-# Share of h bitwise equal to SwiGLU of the exact-rounded gate and up values:
-# h differs where either GEMM output differs from its exact rounding (about
-# 1-2 % each on these inputs, tests/helpers.py), and a differing gate or up
-# value moves h by at most a few bf16 units, which the bound checks.
-H_EQUAL_MIN = 0.95
+# Share of h bitwise equal to SwiGLU of the exact-rounded gate and up values
+# (less three binomial standard deviations for the outputs checked): h differs
+# where either GEMM output differs from its exact rounding (about 1-2 % each
+# on these inputs, tests/helpers.py; measured 0.976-0.983 for h), and a
+# differing gate or up value moves h by at most a few bf16 units, which the
+# bound checks.
+H_EQUAL_MIN = 0.97
 
 SHAPES = [(12288, 4096), (1024, 4096), (1040, 2048), (2048, 12288)]
 
@@ -61,7 +63,7 @@ def test_gate_up_swiglu_h_against_oracle(I, K, M):
     c = helpers.swiglu_criteria(h_bits[rows], xq, sx, helpers.codes_np(wq), sw.cpu().numpy())
     print(f"  h equal {c['equal']:.5f} outside {c['outside']}", flush=True)
     assert c["bound"], (I, K, M, c["outside"])
-    assert c["equal"] >= H_EQUAL_MIN, (I, K, M, c["equal"])
+    assert c["equal"] >= helpers.equal_floor(len(rows) * I, H_EQUAL_MIN), (I, K, M, c["equal"])
     assert np.array_equal(parts.cpu().numpy().view(np.uint16), amax_of(h_bits)), (I, K, M)
 
 
@@ -76,7 +78,7 @@ def test_gate_up_swiglu_h_with_bias_against_oracle():
     xq, sx = oracle.quantize_rows(x[torch.from_numpy(rows).cuda()].float().cpu().numpy())
     c = helpers.swiglu_criteria(helpers.bits(h)[rows], xq, sx, helpers.codes_np(wq), sw.cpu().numpy(),
                                 bias_bits=helpers.bits(bias))
-    assert c["bound"] and c["equal"] >= H_EQUAL_MIN, (c["outside"], c["equal"])
+    assert c["bound"] and c["equal"] >= helpers.equal_floor(len(rows) * I, H_EQUAL_MIN), (c["outside"], c["equal"])
 
 
 class ReferenceSwiGLU(nn.Module):
@@ -148,10 +150,11 @@ def test_reference_mlp_fused_by_fuse_swiglus(M):
     xq, sx = oracle.quantize_rows(x[sel].float().cpu().numpy())
     wcodes = helpers.codes_np(mlp.gate_up.weight)
     c = helpers.swiglu_criteria(helpers.bits(h)[rows], xq, sx, wcodes, mlp.gate_up.scale.cpu().numpy())
-    assert c["bound"] and c["equal"] >= H_EQUAL_MIN, (M, c["outside"], c["equal"])
+    assert c["bound"] and c["equal"] >= helpers.equal_floor(len(rows) * inter, H_EQUAL_MIN), (M, c["outside"], c["equal"])
     hq, hs = oracle.quantize_rows(h[sel].float().cpu().numpy())
     g = helpers.gemm_criteria(helpers.bits(y)[rows], hq, hs, helpers.codes_np(down.weight), down.scale.cpu().numpy())
-    assert g["bound"] and g["finite_match"] and g["equal"] >= helpers.EQUAL_MIN and g["rel_l2"] <= helpers.REL_L2_MAX, g
+    assert g["bound"] and g["finite_match"] and g["rel_l2"] <= helpers.REL_L2_MAX, g
+    assert g["equal"] >= helpers.equal_floor(g["n"], helpers.EQUAL_MIN_SWIGLU_H), g
     # against the unfused module: torch's silu on the device may round a rare
     # h differently, so the outputs agree closely rather than bitwise
     assert oracle.rel_l2(oracle.bf16_to_f32(helpers.bits(y)), oracle.bf16_to_f32(helpers.bits(unfused))) <= 2e-3

@@ -25,8 +25,10 @@ from tests import helpers
 pytestmark = pytest.mark.gpu
 
 
-def check_rows(y, x, wq, sw, rows=None, cols=None):
-    """Oracle criteria (tests/helpers.py) on a sample of token rows and output channels."""
+def check_rows(y, x, wq, sw, rows=None, cols=None, bar=None):
+    """Oracle criteria (tests/helpers.py) on a sample of token rows and output
+    channels; `bar`: the equal-share bar of the input family (default
+    helpers.EQUAL_MIN)."""
     if rows is not None:
         x, y = x[rows], y[rows]
     if cols is not None:
@@ -34,7 +36,7 @@ def check_rows(y, x, wq, sw, rows=None, cols=None):
     xq, sx = oracle.quantize_rows(x.float().cpu().numpy())
     c = helpers.gemm_criteria(helpers.bits(y), xq, sx, helpers.codes_np(wq), sw.cpu().numpy())
     assert c["finite_match"] and c["bound"], c
-    assert c["equal"] >= helpers.EQUAL_MIN and c["rel_l2"] <= helpers.REL_L2_MAX, c
+    assert c["equal"] >= helpers.equal_floor(c["n"], bar or helpers.EQUAL_MIN) and c["rel_l2"] <= helpers.REL_L2_MAX, c
     return c
 
 
@@ -117,7 +119,7 @@ def test_ragged_prefill_then_decode(stack):
         if layer in (0, LAYERS - 1):
             for name in ("q", "k", "v", "o", "gate_up"):
                 check_rows(out[name], h, *weights[name], rows=rows)
-            check_rows(out["down"], out["h_mid"], *weights["down"], rows=rows)
+            check_rows(out["down"], out["h_mid"], *weights["down"], rows=rows, bar=helpers.EQUAL_MIN_SWIGLU_H)
         if layer == 0:
             # packed rows equal each sequence alone (sequences longer than 64 tokens: prefill kernel)
             for i in (0, 17, 63):
@@ -130,7 +132,8 @@ def test_ragged_prefill_then_decode(stack):
                             assert torch.equal(out[name][a:b], alone[name]), (i, name)
                         else:
                             x_in = alone["h_mid"] if name == "down" else h[a:b]
-                            check_rows(alone[name], x_in, *weights[name], rows=torch.arange(0, b - a, 29, device="cuda"))
+                            check_rows(alone[name], x_in, *weights[name], rows=torch.arange(0, b - a, 29, device="cuda"),
+                                       bar=helpers.EQUAL_MIN_SWIGLU_H if name == "down" else None)
         h = rms_normalize(out["down"])
         assert torch.isfinite(h.float()).all()
     # decode: 64 steps at batch 64 through the whole stack
@@ -144,7 +147,7 @@ def test_ragged_prefill_then_decode(stack):
                 first = out
                 for name in ("q", "k", "v", "o", "gate_up"):
                     check_rows(out[name], hs, *weights[name])
-                check_rows(out["down"], out["h_mid"], *weights["down"])
+                check_rows(out["down"], out["h_mid"], *weights["down"], bar=helpers.EQUAL_MIN_SWIGLU_H)
             hs = rms_normalize(out["down"])
         x = hs
     again = run_layer(stack[0], rms_normalize(synthetic.activations_outliers(64, synthetic.HIDDEN, 5500).cuda()))
