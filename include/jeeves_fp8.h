@@ -187,8 +187,11 @@ int jv_fp8_swiglu_quantize(const void* gate, int64_t ldg, const void* up, int64_
  * row stride ldh >= I; h_amax: NULL or [M, I/16] uint16 receiving, per token
  * and 16 channels of h, the largest |h| as a bf16 magnitude pattern (NaN
  * sorts above inf). I a positive multiple of 16, K <= 16384. workspace:
- * jv_fp8_linear_workspace_bytes(M, 2I, K, rank) bytes suffice; the fused
- * GEMM never splits K. The gate+up output [M, 2I] never reaches memory.
+ * jv_fp8_linear_workspace_bytes(M, 2I, K, rank) bytes; tile_counters as for
+ * jv_fp8_linear: the fused GEMM takes the plain GEMM's plan for the same
+ * weight, a K split across workgroups included (the last workgroup of a
+ * tile applies SwiGLU to the summed tile). The gate+up output [M, 2I] never
+ * reaches memory.
  * h follows the reference's F.silu(gate) * up branch (two bf16 roundings);
  * its fla branch (_fla_swiglu, one rounding) is not matched, and parity with
  * it is unpinned. */

@@ -63,7 +63,7 @@ int64_t split_partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
 // The same for the fp8 GEMM's kernel choice: decode split-K partials, or the
 // prefill tiles' split-K partial tiles.
 int64_t partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
-  if (jv::decode_kernel_for(M, N, cus)) return split_partial_bytes(M, N, K, cus);
+  if (jv::fp8_decode_kernel_for(M, N, K, cus)) return split_partial_bytes(M, N, K, cus);
   return round_up(jv::prefill_partial_bytes(jv::prefill_tile(M, N, K, cus), M, N), 256);
 }
 
@@ -84,7 +84,7 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, co
   if ((uint64_t)M * (uint64_t)ldxq >= (1ull << 32) || (uint64_t)jv::packed_x_bytes(M, K) >= (1ull << 32))
     return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
   jv::Epilogue ep{sx, sw, bias, lora_t, lora_b, lora_scaling, y, ldy, swiglu_half, h_amax};
-  if (jv::decode_kernel_for(M, N, cus)) {
+  if (jv::fp8_decode_kernel_for(M, N, K, cus)) {
     const jv::DecodePlan plan = jv::decode_plan(M, N, K, cus, swiglu_half != 0);
     const int splits = plan.splits;
     float* partial = nullptr;
@@ -102,8 +102,9 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, co
                                       stream),
                       "fp8 decode GEMM launch");
   }
-  // The fused SwiGLU GEMM keeps whole k ranges (its callers pass no partials).
-  const jv::PrefillTile tile = jv::prefill_tile(M, N, K, cus, swiglu_half == 0);
+  // The fused SwiGLU GEMM takes the plan of the plain GEMM of the same weight
+  // (a K split included), so its gate and up values are bitwise those.
+  const jv::PrefillTile tile = jv::prefill_tile(M, N, K, cus);
   float* partials = nullptr;
   if (tile.splits > 1) {
     const int64_t tiles = jv::prefill_counters(tile, M, N);
@@ -361,13 +362,13 @@ int jv_fp8_untile_weight(const void* tiled, int64_t N, int64_t K, void* codes, i
 
 int jv_fp8_split_for(int64_t M, int64_t N, int64_t K, int cu_count) {
   if (K <= 0 || N <= 0 || M <= 0 || cu_count <= 0) return 1;
-  if (!jv::decode_kernel_for(M, N, cu_count)) return jv::prefill_tile(M, N, K, cu_count).splits;
+  if (!jv::fp8_decode_kernel_for(M, N, K, cu_count)) return jv::prefill_tile(M, N, K, cu_count).splits;
   return jv::decode_plan(M, N, K, cu_count).splits;
 }
 
 int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count) {
   if (K <= 0 || N <= 0 || M <= 0 || cu_count <= 0) return 0;
-  if (!jv::decode_kernel_for(M, N, cu_count)) return jv::prefill_counters(jv::prefill_tile(M, N, K, cu_count), M, N);
+  if (!jv::fp8_decode_kernel_for(M, N, K, cu_count)) return jv::prefill_counters(jv::prefill_tile(M, N, K, cu_count), M, N);
   const jv::DecodePlan p = jv::decode_plan(M, N, K, cu_count);
   return p.splits > 1 ? p.groups : 0;
 }
@@ -376,7 +377,7 @@ int jv_fp8_launch_shape(int64_t M, int64_t N, int64_t K, int cu_count, int32_t* 
   if (!shape) return fail(JV_ERR_VALUE, "shape needs 4 slots");
   if (int rc = check_gemm_shape(M, N, K)) return rc;
   if (M <= 0 || cu_count <= 0) return fail(JV_ERR_VALUE, "launch shape needs M > 0 and a CU count");
-  if (jv::decode_kernel_for(M, N, cu_count)) {
+  if (jv::fp8_decode_kernel_for(M, N, K, cu_count)) {
     const jv::DecodePlan p = jv::decode_plan(M, N, K, cu_count);
     shape[0] = 0;
     shape[1] = p.groups * p.splits;
@@ -429,7 +430,11 @@ int jv_fp8_linear_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw,
   if (h_amax && (reinterpret_cast<uintptr_t>(h_amax) & 1))
     return fail(JV_ERR_VALUE, "h_amax must be 2-byte aligned (uint16 maxima)");
   if (int rc = check_weight(2 * I, K, ldw, w)) return rc;
-  const int64_t need = round_up(codes_bytes(M, K), 256) + round_up(M * 4, 256) + round_up(M * lora_rank * 4, 256);
+  const int cus = cu_count_of(-1);
+  if (cus <= 0) return fail(JV_ERR_HIP, "cannot query the device's compute units");
+  const int64_t pbytes = partial_bytes(M, 2 * I, K, cus);
+  const int64_t need =
+      round_up(codes_bytes(M, K), 256) + round_up(M * 4, 256) + round_up(M * lora_rank * 4, 256) + pbytes;
   if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255))
     return fail(JV_ERR_VALUE, "workspace needs %lld bytes, 256-byte aligned", (long long)need);
   uint8_t* ws = (uint8_t*)workspace;
@@ -438,14 +443,15 @@ int jv_fp8_linear_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw,
   float* sx = (float*)ws;
   ws += round_up(M * 4, 256);
   float* lora_t = lora_rank ? (float*)ws : nullptr;
+  ws += round_up(M * lora_rank * 4, 256);
   hipStream_t s = (hipStream_t)stream;
   if (int rc = hip_status(jv::quant_rows_bf16((const uint16_t*)x, ldx, M, (int)K, codes, K, sx, (const uint16_t*)lora_a,
                                               (int)lora_rank, lora_t, true, s),
                           "activation quantization launch"))
     return rc;
   return run_gemm(codes, 0, true, sx, (const uint8_t*)w, ldw, w_scale, (const uint16_t*)bias, lora_t,
-                  (const uint16_t*)lora_b, lora_rank, lora_scaling, (uint16_t*)h, ldh, M, 2 * I, K, nullptr, 0,
-                  tile_counters, n_counters, s, I, h_amax);
+                  (const uint16_t*)lora_b, lora_rank, lora_scaling, (uint16_t*)h, ldh, M, 2 * I, K, pbytes ? ws : nullptr,
+                  pbytes, tile_counters, n_counters, s, I, h_amax);
 }
 
 int jv_fp8_quantize_swiglu_output(const void* h, int64_t ldh, const uint16_t* h_amax, int64_t M, int64_t I, void* codes,

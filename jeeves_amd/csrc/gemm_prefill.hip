@@ -1027,7 +1027,23 @@ static hipError_t launch_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* 
 #define JV_PREFILL_LAUNCH_SK_X(R, PW)             \
   if (ldx == 0) JV_PREFILL_LAUNCH_SK(R, PW, true); \
   else JV_PREFILL_LAUNCH_SK(R, PW, false);
-      if (ep.half) return hipErrorInvalidValue;
+      if (ep.half) {
+        // fused SwiGLU, split K: packed activation codes only; the last
+        // workgroup of a tile applies the SwiGLU epilogue to the summed tile
+#define JV_PREFILL_LAUNCH_SK_SW(R, PW)                                        \
+  gemm_prefill_kernel<BM, BN, WGM, WGN, BK, STAGES, R, PW, true, true, true>  \
+      <<<grid, block, 0, stream>>>(xq, ldx, w, ldw, M, N, K, tm, tn, group_m, ep, splits, partials, counters)
+        if (ldx != 0) return hipErrorInvalidValue;
+        if (rank == 16) {
+          if (ldw == 0) JV_PREFILL_LAUNCH_SK_SW(16, true);
+          else JV_PREFILL_LAUNCH_SK_SW(16, false);
+        } else {
+          if (ldw == 0) JV_PREFILL_LAUNCH_SK_SW(0, true);
+          else JV_PREFILL_LAUNCH_SK_SW(0, false);
+        }
+#undef JV_PREFILL_LAUNCH_SK_SW
+        return hipGetLastError();
+      }
       if (rank == 16) {
         if (ldw == 0) { JV_PREFILL_LAUNCH_SK_X(16, true) }
         else { JV_PREFILL_LAUNCH_SK_X(16, false) }
@@ -1141,11 +1157,48 @@ static double lockstep_time_us(const LockstepCost& c, int64_t M, int64_t N, int6
   return t;
 }
 
+// Tiles for 17-128 tokens (the engine's decode batches), measured on the 9B
+// projection shapes (graphs over rotated weights; us at M = 32 / 48 / 64 /
+// 96 / 128). Deeper copy rings than the prefill tiles: these launches are
+// bound by how many bytes each CU keeps in flight, not by the MFMAs.
+//  * weights of 1.5 rounds of 64-channel tiles (gate+up) at up to 64 tokens:
+//    64x128 tiles of 8 waves, 4 stages (21.2 / 22.2 / 23.1 vs 22.0 / 23.0 /
+//    24.1 with 64x64 and 4 stages); above 64 tokens the model below (128x128);
+//  * above 64 tokens, weights of 0.625 rounds of 64x128 tiles (N >= 10240 at
+//    65-128 tokens): 64x128 tiles of 8 waves, 5 stages (10240-wide 17.0 /
+//    17.9 at 96 / 128 vs 18.1 / 19.8 before; 12288-wide 17.7 / 18.6 vs 18.9 /
+//    20.5);
+//  * everything else: 64x64 tiles of 4 waves, 5 stages (80 KB of LDS, one
+//    workgroup per CU), K split so the tiles and splits reach the CUs (at most
+//    4 ways): q/o 10.2 / 10.3 at 96 / 128 vs 11.4 / 11.8; merged q/k/v 12.0 /
+//    12.2 vs 14.2 / 15.1; down 14.9 / 15.4 / 15.8 / 19.5 / 20.4 vs 15.8 /
+//    16.7 / 18.8 / 20.3 / 22.1; k/v 8.4 / 8.5 vs 8.6 / 8.7.
+static bool small_batch_tile(int64_t M, int64_t N, int64_t K, int64_t cus, bool split_k, PrefillTile& t) {
+  const int64_t mt = (M + 63) / 64, n64 = (N + 63) / 64, t64 = mt * n64, t128 = mt * ((N + 127) / 128);
+  if (2 * n64 >= 3 * cus) {
+    if (M > kDecodeMaxRows) return false;
+    t = PrefillTile{64, 128, 2, 4, 128, 4, 8};
+    return true;
+  }
+  if (M > kDecodeMaxRows && 8 * t128 >= 5 * cus) {
+    t = PrefillTile{64, 128, 2, 4, 128, 5, 8};
+    return true;
+  }
+  t = PrefillTile{64, 64, 2, 2, 128, 5, 8};
+  if (split_k && 8 * t64 < 5 * cus) {
+    // each split keeps at least four 128-deep stages, the partials at most
+    // kMaxPrefillPartialBytes (a split's partials are one fp32 64x64 tile per tile)
+    int s = (int)(cus / t64);
+    s = s < 1 ? 1 : (s > 4 ? 4 : s);
+    while (s > 1 && (K / t.bk < 4 * s || t64 * s * 64 * 64 * 4 > kMaxPrefillPartialBytes)) --s;
+    t.splits = s;
+  }
+  return true;
+}
+
 PrefillTile prefill_tile(int64_t M, int64_t N, int64_t K, int cu_count, bool split_k) {
-  // Batches of at most 64 tokens that reach the prefill kernel (wide weights,
-  // decode_kernel_for) take 64x64 tiles: 23.4 us for gate+up at M = 64 vs
-  // 25.9 with 64x128 and 45.9 with 128x64.
-  if (M <= kDecodeMaxRows) return {64, 64, 2, 2, 128, 4, 8};
+  PrefillTile small;
+  if (M <= 2 * kDecodeMaxRows && small_batch_tile(M, N, K, cu_count, split_k, small)) return small;
   // 256x256 tiles in the ping-pong form (least L2 -> LDS traffic per flop,
   // and the fastest tile per CU) once they cover five eighths of the CUs,
   // even in a partial round: gate+up at M = 512 (192 tiles) 52.7 us against
@@ -1196,6 +1249,9 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
   JV_PREFILL_CASE(256, 128, 2, 4, 128, 3)
   JV_PREFILL_CASE(128, 128, 2, 2, 128, 4)
   JV_PREFILL_CASE(64, 64, 2, 2, 128, 4)
+  JV_PREFILL_CASE(64, 64, 2, 2, 128, 5)
+  JV_PREFILL_CASE(64, 128, 2, 4, 128, 4)
+  JV_PREFILL_CASE(64, 128, 2, 4, 128, 5)
 #undef JV_PREFILL_CASE
   return hipErrorInvalidValue;
 }

@@ -11,17 +11,41 @@ namespace jv {
 // Decode regime: M <= kDecodeMaxRows tokens.
 constexpr int kDecodeMaxRows = 64;
 
-// The decode kernel takes M <= 16 tokens, and up to kDecodeMaxRows tokens
-// unless the weight is wide enough for 1.5 rounds of 64-channel tiles of the
-// prefill kernel (measured on MI355X: gate+up, N = 24576, 23.4 vs 30.4 us at
-// M = 64, 23.1 vs 28.7 at M = 40, 21.6 vs 22.4 at M = 24; the lm_head,
-// N = 248320, 193 vs 236 us at M = 64 and 179 vs 202 at M = 32; q/o, k/v and
-// down stay on the decode kernel, 1.4-1.8x faster there). Those prefill
-// tiles stage each 16-token tile's codes in LDS once per workgroup, where
-// the decode waves each load every code fragment.
+// The W8A16 parity mode's base rule: its decode kernel takes M <= 16 tokens,
+// and up to kDecodeMaxRows tokens unless the weight is wide enough for 1.5
+// rounds of 64-channel tiles of the prefill kernel (measured on MI355X:
+// gate+up, N = 24576, 23.4 vs 30.4 us at M = 64 on the FP8 kernels, 23.1 vs
+// 28.7 at M = 40, 21.6 vs 22.4 at M = 24; the lm_head, N = 248320, 193 vs 236
+// us at M = 64 and 179 vs 202 at M = 32). Those prefill tiles stage each
+// 16-token tile's codes in LDS once per workgroup, where the decode waves each
+// load every code fragment.
 inline bool decode_kernel_for(int64_t M, int64_t N, int cu_count) {
   if (M > kDecodeMaxRows) return false;
   return M <= 16 || 2 * ((N + 63) / 64) < 3 * (int64_t)cu_count;
+}
+
+// The FP8 GEMM's rule: the decode kernel at 1-16 tokens, and at 17-64 tokens
+// except on weights wide enough for 1.5 rounds of 64-channel tiles (gate+up,
+// the lm_head) and, from 32 tokens, on weights of at least 0.625 rounds
+// (N >= 10240: the 9B model's attention and drafter merged projections) or
+// long rows whose 64-channel tiles, split K four ways, fill the CUs (K >=
+// 8192: down). There every decode workgroup would re-read all M x K
+// activation codes from L2 for its 16 or 32 channels -- the time grows by
+// about 1 us per 16 tokens on q/o and 2.6 us on down, whatever the plan --
+// while the prefill kernel's 64-token tiles share each code fragment among
+// 64 or 128 channels. Measured (graphs over rotated weights, us, decode kernel
+// vs 64x64 tiles with a 5-stage ring): down M = 32 / 48 / 64: 15.8 / 16.7 /
+// 18.8 vs 14.9 / 15.4 / 15.8; the 12288-wide projection 15.1 / 16.8 / 19.1
+// vs 13.3 / 14.0 / 14.1; the 10240-wide 13.1 / 15.8 / 18.4 vs 12.6 / 13.1 /
+// 13.3; q/o, k/v, merged q/k/v and the 8192-wide stay on the decode kernel
+// (q M = 64: 8.4 vs 9.4).
+inline bool fp8_decode_kernel_for(int64_t M, int64_t N, int64_t K, int cu_count) {
+  if (M > kDecodeMaxRows) return false;
+  if (M <= 16) return true;
+  const int64_t t64 = (N + 63) / 64, cus = cu_count;
+  if (2 * t64 >= 3 * cus) return false;
+  if (M >= 32 && (8 * t64 >= 5 * cus || (K >= 8192 && 4 * t64 >= cus))) return false;
+  return true;
 }
 
 // The W8A16 prefill tiles stage bf16 token rows, twice the bytes of codes,
@@ -128,10 +152,11 @@ hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, bool packed_x, const uin
                        const DecodePlan& plan, float* partial, int* counters, const Epilogue& ep, int rank,
                        hipStream_t stream);
 
-// split_k = false: plans without K splits only (the fused SwiGLU epilogue).
+// split_k = false: plans without K splits only.
 PrefillTile prefill_tile(int64_t M, int64_t N, int64_t K, int cu_count, bool split_k = true);
 // ldx = 0: packed activation codes (packed_x_offset); ldw = 0: tiled weights.
-// ep.half != 0: fused SwiGLU epilogue (packed codes only, N = 2 half).
+// ep.half != 0: fused SwiGLU epilogue (packed codes only, N = 2 half; with a
+// K split on the lockstep tiles the last workgroup of a tile applies it).
 // With tile.splits > 1: partials of prefill_partial_bytes and
 // prefill_counters zeroed tile counters (left at zero).
 hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,

@@ -408,6 +408,7 @@ def gate_up_swiglu(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *
         scale = scale.to(torch.float32).contiguous()
         L = _lib.lib()
         with torch.cuda.device(dev):
+            counters = _tile_counters(dev, M, N, K)
             ws_bytes = L.jv_fp8_linear_workspace_bytes(M, N, K, rank)
             if ws_bytes < 0:
                 _lib.check(_lib.JV_ERR_HIP)
@@ -416,7 +417,8 @@ def gate_up_swiglu(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *
                                               bias.data_ptr() if bias is not None else None, a.data_ptr() if rank else None,
                                               b.data_ptr() if rank else None, rank, scaling, h.data_ptr(), I,
                                               parts.data_ptr() if parts is not None else None, M, I, K, ws.data_ptr(),
-                                              ws_bytes, None, 0, _stream(dev)))
+                                              ws_bytes, _lib.counters_ptr(counters),
+                                              counters.numel() if counters is not None else 0, _stream(dev)))
     return (h, parts) if amax else h
 
 

@@ -84,12 +84,18 @@ def test_split_for_is_pure_host_logic(product_lib):
     assert L.jv_fp8_split_for(16, 128, 12288, 256) == 12  # 8 tiles; K=12288 runs 8 waves: capped at K/128/8
     assert L.jv_fp8_counters_needed(16, 256, 4096, 256) == 16
     assert L.jv_fp8_counters_needed(16, 4096, 4096, 256) == 0
-    # prefill: the lockstep tile and K split of least modelled time; a split
-    # keeps at least four 128-deep stages, at most 8
-    assert L.jv_fp8_split_for(96, 4096, 4096, 256) == 4     # 128 tiles of 64x64
+    # 17-128 tokens on the prefill kernel: 64x64 tiles (5 stages) split K
+    # until tiles x splits reach the CUs, at most 4 ways, none from 0.625
+    # rounds of tiles; longer rows take 64 tokens x 64 channels per tile too
+    assert L.jv_fp8_split_for(96, 4096, 4096, 256) == 2     # 128 tiles of 64x64
     assert L.jv_fp8_counters_needed(96, 4096, 4096, 256) == 128
-    assert L.jv_fp8_split_for(96, 4096, 12288, 256) == 4
-    assert L.jv_fp8_split_for(96, 6144, 4096, 256) == 2     # 192 tiles
+    assert L.jv_fp8_split_for(96, 4096, 12288, 256) == 2
+    assert L.jv_fp8_split_for(96, 6144, 4096, 256) == 1     # 192 tiles
+    assert L.jv_fp8_split_for(64, 4096, 12288, 256) == 4    # down from 32 tokens: 64 tiles of 64x64
+    assert L.jv_fp8_counters_needed(64, 4096, 12288, 256) == 64
+    assert L.jv_fp8_split_for(31, 4096, 12288, 256) == 1    # below 32 tokens: the decode kernel
+    # above 128 tokens: the lockstep tile and K split of least modelled time; a
+    # split keeps at least four 128-deep stages, at most 8
     assert L.jv_fp8_split_for(256, 4096, 12288, 256) == 4   # 64 tiles of 128x128
     assert L.jv_fp8_counters_needed(256, 4096, 12288, 256) == 64
     assert L.jv_fp8_split_for(512, 4096, 12288, 256) == 2   # 128 tiles of 128x128

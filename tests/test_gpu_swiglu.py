@@ -210,8 +210,10 @@ def test_fused_swiglu_writes_stay_inside_h_and_amax(M):
     L = _lib.lib()
     ws_bytes = L.jv_fp8_linear_workspace_bytes(M, N, K, 0)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    counters = torch.zeros(65536, dtype=torch.int32, device="cuda")
     _lib.check(L.jv_fp8_linear_swiglu(x.data_ptr(), K, wq.data_ptr(), K, sw.data_ptr(), None, None, None, 0, 0.0,
-                                      h.data_ptr(), ldh, parts.data_ptr(), M, I, K, ws.data_ptr(), ws_bytes, None, 0,
+                                      h.data_ptr(), ldh, parts.data_ptr(), M, I, K, ws.data_ptr(), ws_bytes,
+                                      _lib.counters_ptr(counters), counters.numel(),
                                       torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()
     assert torch.equal(h[:M, I:], guard_h[:M, I:]) and torch.equal(h[M:], guard_h[M:])
