@@ -1,5 +1,5 @@
 // C ABI of libjeeves_fp8.so (declared in include/jeeves_fp8.h): argument
-// validation, regime dispatch (decode vs prefill), workspace carving, and
+// validation, regime dispatch (decode, batch-decode, prefill), workspace carving, and
 // per-thread error messages. Launches only; no allocation, no host sync.
 #include <atomic>
 #include <cstdarg>
@@ -63,6 +63,7 @@ int64_t split_partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
 // The same for the fp8 GEMM's kernel choice: decode split-K partials, or the
 // prefill tiles' split-K partial tiles.
 int64_t partial_bytes(int64_t M, int64_t N, int64_t K, int cus) {
+  if (jv::batch_plan(M, N, K, cus, false, nullptr)) return 0;
   if (jv::fp8_decode_kernel_for(M, N, K, cus)) return split_partial_bytes(M, N, K, cus);
   return round_up(jv::prefill_partial_bytes(jv::prefill_tile(M, N, K, cus), M, N), 256);
 }
@@ -84,6 +85,10 @@ int run_gemm(const uint8_t* xq, int64_t ldxq, bool packed_x, const float* sx, co
   if ((uint64_t)M * (uint64_t)ldxq >= (1ull << 32) || (uint64_t)jv::packed_x_bytes(M, K) >= (1ull << 32))
     return fail(JV_ERR_VALUE, "operands above 4 GiB are not supported");
   jv::Epilogue ep{sx, sw, bias, lora_t, lora_b, lora_scaling, y, ldy, swiglu_half, h_amax};
+  jv::BatchPlan batch;
+  if (jv::batch_plan(M, N, K, cus, swiglu_half != 0, &batch))
+    return hip_status(jv::gemm_batch(xq, ldxq, packed_x, w, ldw, (int)M, (int)N, (int)K, batch, ep, (int)rank, stream),
+                      "fp8 batch GEMM launch");
   if (jv::fp8_decode_kernel_for(M, N, K, cus)) {
     const jv::DecodePlan plan = jv::decode_plan(M, N, K, cus, swiglu_half != 0);
     const int splits = plan.splits;
@@ -362,12 +367,14 @@ int jv_fp8_untile_weight(const void* tiled, int64_t N, int64_t K, void* codes, i
 
 int jv_fp8_split_for(int64_t M, int64_t N, int64_t K, int cu_count) {
   if (K <= 0 || N <= 0 || M <= 0 || cu_count <= 0) return 1;
+  if (jv::batch_plan(M, N, K, cu_count, false, nullptr)) return 1;
   if (!jv::fp8_decode_kernel_for(M, N, K, cu_count)) return jv::prefill_tile(M, N, K, cu_count).splits;
   return jv::decode_plan(M, N, K, cu_count).splits;
 }
 
 int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count) {
   if (K <= 0 || N <= 0 || M <= 0 || cu_count <= 0) return 0;
+  if (jv::batch_plan(M, N, K, cu_count, false, nullptr)) return 0;
   if (!jv::fp8_decode_kernel_for(M, N, K, cu_count)) return jv::prefill_counters(jv::prefill_tile(M, N, K, cu_count), M, N);
   const jv::DecodePlan p = jv::decode_plan(M, N, K, cu_count);
   return p.splits > 1 ? p.groups : 0;
@@ -377,6 +384,14 @@ int jv_fp8_launch_shape(int64_t M, int64_t N, int64_t K, int cu_count, int32_t* 
   if (!shape) return fail(JV_ERR_VALUE, "shape needs 4 slots");
   if (int rc = check_gemm_shape(M, N, K)) return rc;
   if (M <= 0 || cu_count <= 0) return fail(JV_ERR_VALUE, "launch shape needs M > 0 and a CU count");
+  jv::BatchPlan b;
+  if (jv::batch_plan(M, N, K, cu_count, false, &b)) {
+    shape[0] = 3;
+    shape[1] = b.groups * b.msplit;
+    shape[2] = 64 * b.waves;
+    shape[3] = 1;
+    return JV_OK;
+  }
   if (jv::fp8_decode_kernel_for(M, N, K, cu_count)) {
     const jv::DecodePlan p = jv::decode_plan(M, N, K, cu_count);
     shape[0] = 0;

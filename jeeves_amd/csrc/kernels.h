@@ -59,6 +59,80 @@ inline bool w8a16_decode_kernel_for(int64_t M, int64_t N, int cu_count) {
   return M < 32 || decode_kernel_for(M, N, cu_count);
 }
 
+// Batch-decode kernel (gemm_batch.hip) for 17-128 tokens: W waves of `steps`
+// 128-deep k steps cover each row exactly, every wave holding its whole k
+// range of weights in registers; a workgroup takes rt 16-row weight tiles and
+// mt 16-token tiles, and msplit workgroups share each weight group, one part
+// of the batch each.
+struct BatchPlan {
+  int waves, steps;  // waves * steps = K / 128
+  int rt, mt;        // weight tiles and token tiles per workgroup
+  int msplit;        // token parts: mt * msplit = ceil(M / 16)
+  int groups;        // weight groups: ceil(ceil(N / 16) / rt)
+};
+
+// Token tiles a batch workgroup can hold beside its weights without spilling.
+inline int batch_max_mt(int waves, int rt) { return waves == 4 ? 4 : (rt == 1 ? 2 : 1); }
+
+// The batch plan for these sizes, if the batch kernel takes them. Rows of
+// 32 k steps (K = 4096) run as 4 waves x 8, rows of 96 (K = 12288) as
+// 8 x 12: the decode kernel's waves per row at those K, so both give each
+// output the same k order. The plan takes at most one workgroup per CU and
+// at least half the CUs, from weights of 64 tiles up, and minimises the
+// bytes a workgroup reads, (rt + mt) x 16 x K, keeping it within 6 tiles and
+// 576 KiB; ties take one tile per wave. Measured on MI355X (graphs over
+// rotated weights, us, this plan vs the decode or prefill plan it replaces):
+// k/v (1024 x 4096) M = 32 / 64 / 128: 4.2 / 4.2 / 4.7 vs 5.7 / 7.8 / 8.5;
+// q/o (4096 x 4096) M = 64 / 128: 6.9 / 8.7 vs 8.3 / 10.4; merged q/k/v
+// (6144 x 4096) M = 32 / 64: 7.8 / 9.5 vs 8.8 / 10.4; down (4096 x 12288)
+// M = 32: 13.6 vs 14.9. Wider weights, longer token tiles and K = 12288
+// past 32 tokens stay on the decode and prefill plans, which share each
+// activation fragment among more channels (gate+up M = 64: 27 vs 23 us).
+// swiglu: the fused SwiGLU GEMM's plan (a gate/up tile pair per workgroup,
+// the plain plan's waves and steps, hence the plain plan's sums).
+inline bool batch_plan(int64_t M, int64_t N, int64_t K, int cu_count, bool swiglu, BatchPlan* out) {
+  if (M < 17 || M > 128 || N <= 0 || cu_count <= 0) return false;
+  BatchPlan p{};
+  if (K == 32 * 128) {
+    p.waves = 4;
+    p.steps = 8;
+  } else if (K == 96 * 128) {
+    p.waves = 8;
+    p.steps = 12;
+  } else {
+    return false;
+  }
+  const int64_t tiles = (N + 15) / 16, mtall = (M + 15) / 16, cus = cu_count;
+  if (tiles < 64) return false;
+  int64_t best = 0;
+  for (int rt = 1; rt <= 2; ++rt)
+    for (int64_t ms = 1; ms <= mtall; ++ms) {
+      if (mtall % ms) continue;
+      const int64_t mt = mtall / ms, groups = (tiles + rt - 1) / rt, cost = rt + mt;
+      if (mt > batch_max_mt(p.waves, rt) || groups * ms > cus || 2 * groups * ms < cus) continue;
+      if (cost > 6 || cost * K > 36864) continue;
+      if (best == 0 || cost < best) {
+        best = cost;
+        p.rt = rt;
+        p.mt = (int)mt;
+        p.msplit = (int)ms;
+        p.groups = (int)groups;
+      }
+    }
+  if (best == 0) return false;
+  if (swiglu) {
+    // Any tiling of the same waves and steps sums alike: pairs of tiles, the
+    // fewest token parts whose tiles fit beside them.
+    p.rt = 2;
+    p.groups = (int)((tiles + 1) / 2);
+    for (p.msplit = 1; mtall % p.msplit || mtall / p.msplit > batch_max_mt(p.waves, 2); ++p.msplit) {
+    }
+    p.mt = (int)(mtall / p.msplit);
+  }
+  if (out) *out = p;
+  return true;
+}
+
 struct DecodePlan {
   int rt;      // 16-row tiles per wave
   int waves;   // waves per workgroup, splitting the workgroup's k range
@@ -151,6 +225,12 @@ DecodePlan decode_plan(int64_t M, int64_t N, int64_t K, int cu_count, bool swigl
 hipError_t gemm_decode(const uint8_t* xq, int64_t ldxq, bool packed_x, const uint8_t* w, int64_t ldw, int M, int N, int K,
                        const DecodePlan& plan, float* partial, int* counters, const Epilogue& ep, int rank,
                        hipStream_t stream);
+
+// The batch-decode kernel on a batch_plan plan (no workspace, no counters);
+// ldxq = 0 with packed_x: packed codes; ldw = 0: tiled weights; ep.half != 0:
+// fused SwiGLU (packed codes, a batch_plan(..., swiglu = true) plan).
+hipError_t gemm_batch(const uint8_t* xq, int64_t ldxq, bool packed_x, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                      const BatchPlan& p, const Epilogue& ep, int rank, hipStream_t stream);
 
 // split_k = false: plans without K splits only.
 PrefillTile prefill_tile(int64_t M, int64_t N, int64_t K, int cu_count, bool split_k = true);

@@ -84,22 +84,24 @@ def test_split_for_is_pure_host_logic(product_lib):
     assert L.jv_fp8_split_for(16, 128, 12288, 256) == 12  # 8 tiles; K=12288 runs 8 waves: capped at K/128/8
     assert L.jv_fp8_counters_needed(16, 256, 4096, 256) == 16
     assert L.jv_fp8_counters_needed(16, 4096, 4096, 256) == 0
+    # 17-128 tokens on the batch-decode kernel: no K split, no counters
+    assert L.jv_fp8_split_for(96, 4096, 4096, 256) == 1
+    assert L.jv_fp8_counters_needed(96, 4096, 4096, 256) == 0
     # 17-128 tokens on the prefill kernel: 64x64 tiles (5 stages) split K
     # until tiles x splits reach the CUs, at most 4 ways, none from 0.625
     # rounds of tiles; longer rows take 64 tokens x 64 channels per tile too
-    assert L.jv_fp8_split_for(96, 4096, 4096, 256) == 2     # 128 tiles of 64x64
-    assert L.jv_fp8_counters_needed(96, 4096, 4096, 256) == 128
-    assert L.jv_fp8_split_for(96, 4096, 12288, 256) == 2
+    assert L.jv_fp8_split_for(96, 4096, 12288, 256) == 2     # 128 tiles of 64x64
+    assert L.jv_fp8_counters_needed(96, 4096, 12288, 256) == 128
     assert L.jv_fp8_split_for(96, 6144, 4096, 256) == 1     # 192 tiles
     assert L.jv_fp8_split_for(64, 4096, 12288, 256) == 4    # down from 32 tokens: 64 tiles of 64x64
     assert L.jv_fp8_counters_needed(64, 4096, 12288, 256) == 64
-    assert L.jv_fp8_split_for(31, 4096, 12288, 256) == 1    # below 32 tokens: the decode kernel
+    assert L.jv_fp8_split_for(31, 4096, 12288, 256) == 1    # below 32 tokens: the batch-decode kernel
     # above 128 tokens: the lockstep tile and K split of least modelled time; a
     # split keeps at least four 128-deep stages, at most 8
     assert L.jv_fp8_split_for(256, 4096, 12288, 256) == 4   # 64 tiles of 128x128
     assert L.jv_fp8_counters_needed(256, 4096, 12288, 256) == 64
     assert L.jv_fp8_split_for(512, 4096, 12288, 256) == 2   # 128 tiles of 128x128
-    assert L.jv_fp8_split_for(128, 1024, 4096, 256) == 4    # 32 tiles
+    assert L.jv_fp8_split_for(128, 1024, 8192, 256) == 4    # 32 tiles
     assert L.jv_fp8_split_for(256, 1024, 512, 256) == 1     # 4 stages of 128 leave no room to split
     assert L.jv_fp8_split_for(512, 1024, 4096, 256) == 4    # 128 tiles
     assert L.jv_fp8_split_for(512, 4096, 4096, 256) == 1    # 512 tiles fill the CUs
@@ -108,6 +110,40 @@ def test_split_for_is_pure_host_logic(product_lib):
     assert L.jv_fp8_counters_needed(2048, 4096, 4096, 256) == 0
     assert L.jv_fp8_split_for(65, 24576, 4096, 256) == 1    # 192 tiles of 128x128
     assert L.jv_fp8_split_for(4096, 24576, 4096, 256) == 1  # 256x256 ping-pong tiles never split
+
+
+def launch_shape(L, M, N, K, cus=256):
+    shape = (ctypes.c_int32 * 4)()
+    _lib.check(L.jv_fp8_launch_shape(M, N, K, cus, shape))
+    return list(shape)
+
+
+def test_batch_decode_plans_are_host_logic(product_lib):
+    """17-128 tokens on K = 4096 (4 waves of 8 steps) or K = 12288 (8 waves of
+    12): the batch-decode kernel (kind 3) where at most one workgroup per CU,
+    at least half the CUs and at most 6 tiles per workgroup (576 KiB of
+    operands) allow it; one workgroup per weight group and token part."""
+    L = product_lib
+    assert launch_shape(L, 32, 1024, 4096) == [3, 128, 256, 1]     # k/v: 64 groups x 2 token parts
+    assert launch_shape(L, 64, 1024, 4096) == [3, 256, 256, 1]     # 64 x 4 parts of one tile
+    assert launch_shape(L, 128, 1024, 4096) == [3, 256, 256, 1]    # 64 x 4 parts of two tiles
+    assert launch_shape(L, 64, 4096, 4096) == [3, 256, 256, 1]     # q/o: 128 pairs of tiles x 2 parts
+    assert launch_shape(L, 64, 6144, 4096) == [3, 192, 256, 1]     # merged q/k/v: 192 pairs, 4 token tiles
+    assert launch_shape(L, 32, 4096, 12288) == [3, 256, 512, 1]    # down, 8 waves
+    assert launch_shape(L, 16, 1024, 4096)[0] == 0                 # 16 tokens: the decode kernel
+    assert launch_shape(L, 129, 1024, 4096)[0] == 1                # past 128 tokens: prefill tiles
+    assert launch_shape(L, 64, 1024, 2048)[0] != 3                 # other row lengths
+    assert launch_shape(L, 48, 4096, 12288)[0] == 1                # 3 token tiles of K = 12288 exceed 576 KiB
+    assert launch_shape(L, 96, 6144, 4096)[0] == 1                 # 6 token tiles: 7+ tiles a workgroup
+    assert launch_shape(L, 32, 10240, 4096)[0] == 1                # 320 pairs exceed the CUs
+    assert launch_shape(L, 64, 24576, 4096)[0] == 1                # gate+up
+    assert launch_shape(L, 64, 512, 4096)[0] == 0                  # 32 tiles: decode kernel, K split
+    for M in range(17, 129):
+        for N, K in ((1024, 4096), (4096, 4096), (6144, 4096), (4096, 12288)):
+            kind, wgs, threads, splits = launch_shape(L, M, N, K)
+            if kind == 3:
+                assert wgs <= 256 and 2 * wgs >= 256 and splits == 1, (M, N, K)
+                assert L.jv_fp8_counters_needed(M, N, K, 256) == 0 and L.jv_fp8_split_for(M, N, K, 256) == 1
 
 
 def test_wide_weights_never_split_k(product_lib):

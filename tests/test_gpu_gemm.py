@@ -176,7 +176,7 @@ def test_split_k_decode_path(N, K, M):
     assert all(int(c.abs().sum()) == 0 for c in TILE_COUNTERS.values())
 
 
-@pytest.mark.parametrize("N,K,M", [(4096, 4096, 96), (4096, 12288, 128), (1024, 4096, 65), (1024, 4096, 512),
+@pytest.mark.parametrize("N,K,M", [(4096, 8192, 96), (4096, 12288, 128), (1024, 8192, 65), (1024, 4096, 512),
                                    (128, 4096, 2048), (1040, 4096, 200), (4096, 12288, 256), (4096, 12288, 512),
                                    (4112, 12288, 300), (2064, 12288, 333)])
 def test_split_k_prefill_path(N, K, M):
