@@ -241,7 +241,8 @@ int jv_fp8_split_for(int64_t M, int64_t N, int64_t K, int cu_count);
 int64_t jv_fp8_counters_needed(int64_t M, int64_t N, int64_t K, int cu_count);
 
 /* The same introspection for the whole launch: shape[0] = the GEMM kernel
- * (0 decode, 1 prefill lockstep tiles, 2 prefill ping-pong tiles), shape[1] =
+ * (0 decode, 1 prefill lockstep tiles, 2 prefill ping-pong tiles, 3 batch-decode
+ * kernel: 17-128 tokens, no K split, no counters), shape[1] =
  * its workgroups (K splits included), shape[2] = threads per workgroup,
  * shape[3] = K splits across workgroups. For measurement tools that
  * compare a GEMM with other launches of its shape. */
