@@ -108,6 +108,32 @@ def test_batch_rows_equal_decode_kernel_slices(N, K, M):
                                       for i in range(0, M, 16)]))
 
 
+@pytest.mark.parametrize("N,K", [(1024, 4096), (4096, 4096), (6144, 4096), (4096, 12288)])
+def test_batch_every_token_count(N, K):
+    """Every token count of 17-128 that takes a batch plan on these weights
+    (each token split and tile shape the plan picks): the batch equals its
+    16-token slices on the decode kernel bit for bit where the decode kernel
+    runs the same waves per row (one 16-row tile per wave), else the oracle
+    criteria on the first and last rows."""
+    wq, sw = quantize_rows(synthetic.weight(N, K, 9250).cuda())
+    wt = tile_weight(wq)
+    x_all = synthetic.activations_heavy_tail(128, K, 9251).cuda()
+    same_waves = N <= 4096  # the decode plan takes one tile per wave here (merged q/k/v: two, eight waves)
+    ran = 0
+    for M in range(17, 129):
+        if launch_shape(M, N, K)[0] != 3:
+            continue
+        ran += 1
+        x = x_all[:M]
+        y = fp8_matmul(x, wt, sw, tiled=True)
+        if same_waves:
+            assert torch.equal(y, torch.cat([fp8_matmul(x[i:i + 16], wt, sw, tiled=True) for i in range(0, M, 16)])), M
+        else:
+            rows = torch.tensor([0, M - 1], device="cuda")
+            check(y[rows], x[rows], wq, sw)
+    assert ran >= 16, ran
+
+
 @pytest.mark.parametrize("N,K,M", [(1036, 4096, 40), (1024, 4096, 100), (4096, 12288, 20)])
 def test_batch_writes_stay_inside_the_output(N, K, M):
     """Through the C ABI with a row stride past N and a sentinel-filled guard

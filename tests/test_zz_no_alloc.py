@@ -77,14 +77,16 @@ def test_first_noalloc_call_captured_in_a_graph():
         assert torch.equal(y, want), rep
 
 
-# (N, K, first M, second M, tiled, bias, lora): split-K decode, plain decode,
-# 64x64 prefill tiles on a wide weight, split-K 64x64 prefill tiles (4
-# splits), split-K 128x128 prefill tiles (2 and 4 splits, 16 MiB of
-# partials), lockstep and ping-pong prefill tiles.
+# (N, K, first M, second M, tiled, bias, lora): split-K decode, batch-decode
+# then plain decode, 64x64 prefill tiles on a wide weight, split-K 64x64
+# prefill tiles (4 splits), split-K 128x128 prefill tiles (2 and 4 splits,
+# 16 MiB of partials), lockstep and ping-pong prefill tiles, batch-decode on
+# row-major weights with LoRA.
 CASES = [(256, 4096, 16, 5, False, False, False), (4096, 4096, 64, 1, True, True, False),
          (24576, 4096, 48, 17, True, False, False), (1024, 4096, 300, 65, True, True, True),
          (4096, 12288, 96, 128, False, False, False), (4096, 12288, 512, 256, True, False, True),
-         (24576, 4096, 2048, 256, True, False, True), (4096, 12288, 33, 16, False, True, False)]
+         (24576, 4096, 2048, 256, True, False, True), (4096, 12288, 33, 16, False, True, False),
+         (1024, 4096, 100, 40, False, True, True)]
 
 
 @pytest.mark.parametrize("N,K,M1,M2,tiled,use_bias,use_lora", CASES)
