@@ -37,8 +37,11 @@ inline bool decode_kernel_for(int64_t M, int64_t N, int cu_count) {
 // vs 64x64 tiles with a 5-stage ring): down M = 32 / 48 / 64: 15.8 / 16.7 /
 // 18.8 vs 14.9 / 15.4 / 15.8; the 12288-wide projection 15.1 / 16.8 / 19.1
 // vs 13.3 / 14.0 / 14.1; the 10240-wide 13.1 / 15.8 / 18.4 vs 12.6 / 13.1 /
-// 13.3; q/o, k/v, merged q/k/v and the 8192-wide stay on the decode kernel
-// (q M = 64: 8.4 vs 9.4).
+// 13.3; q/o, k/v, merged q/k/v and the 8192-wide stayed on the decode kernel
+// (q M = 64: 8.4 vs 9.4). The batch-decode plan (batch_plan, below) is asked
+// first and takes most of those: the decode kernel now runs 17-64 tokens
+// only where neither it nor the prefill tiles do (the 10240/12288-wide
+// projections at 17-31 tokens, other K).
 inline bool fp8_decode_kernel_for(int64_t M, int64_t N, int64_t K, int cu_count) {
   if (M > kDecodeMaxRows) return false;
   if (M <= 16) return true;
@@ -80,7 +83,7 @@ inline int batch_max_mt(int waves, int rt) { return waves == 4 ? 4 : (rt == 1 ? 
 // output the same k order. The plan takes at most one workgroup per CU and
 // at least half the CUs, from weights of 64 tiles up, and minimises the
 // bytes a workgroup reads, (rt + mt) x 16 x K, keeping it within 6 tiles and
-// 576 KiB; ties take one tile per wave. Measured on MI355X (graphs over
+// 576 KiB; ties take one weight tile per workgroup. Measured on MI355X (graphs over
 // rotated weights, us, this plan vs the decode or prefill plan it replaces):
 // k/v (1024 x 4096) M = 32 / 64 / 128: 4.2 / 4.2 / 4.7 vs 5.7 / 7.8 / 8.5;
 // q/o (4096 x 4096) M = 64 / 128: 6.9 / 8.7 vs 8.3 / 10.4; merged q/k/v

@@ -11,10 +11,12 @@ kernels of ``libjeeves_fp8.so``, called through its C ABI:
   to fp16 with a power-of-two row scale (``inference/fp8.py:46-58``);
 * the GEMM multiplies e4m3 by e4m3 on the FP8 MFMA units and applies
   ``acc * sx[m] * sw[n]`` (+ bias, + optional LoRA) in its epilogue;
-* M <= ``DECODE_MAX_ROWS`` runs the HBM-bound split-K decode kernel, larger M
-  the LDS-tiled prefill kernel; batches of 17-64 tokens on weights wide enough
-  for 1.5 rounds of 64-channel tiles (gate+up, the lm_head) take the prefill
-  kernel's 64x64 tiles, which load each code fragment once per workgroup.
+* 1-16 tokens run the HBM-bound split-K decode kernel; 17-128 tokens the
+  batch-decode kernel on weights of up to one round of workgroups at
+  K = 4096 / 12288 (whole k ranges of weights in registers, the batch's token
+  tiles split across workgroups), else deep-ring 64x64 / 64x128 prefill tiles
+  (gate+up, the lm_head, down past 32 tokens); larger batches the LDS-tiled
+  prefill kernels. ``jv_fp8_launch_shape`` reports the plan for a shape.
 
 Everything is enqueued on ``torch.cuda.current_stream()`` without host
 synchronisation; outputs and workspaces come from torch's caching allocator
@@ -30,9 +32,9 @@ from . import _lib
 from .device import sm_count
 from .fp8_weights import FP8, quantize_rows
 
-# Rows at or below which fp8_matmul takes the decode kernel (the role of
-# SPLIT_K_MAX_ROWS, inference/fp8.py:20): up to four 16-token MFMA column tiles
-# (above 16 rows only on weights too narrow for 1.5 rounds of 64x64 prefill tiles).
+# Decode batches (the role of SPLIT_K_MAX_ROWS, inference/fp8.py:20): up to
+# four 16-token MFMA column tiles; the quantizer of h reads the SwiGLU
+# epilogue's maxima at these sizes, and warm() covers them.
 DECODE_MAX_ROWS = 64
 # Longest row the single-pass quantizer (and so the packed code layout) covers.
 QUANT_MAX_PACKED_COLS = 16384
