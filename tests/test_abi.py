@@ -146,6 +146,28 @@ def test_batch_decode_plans_are_host_logic(product_lib):
                 assert L.jv_fp8_counters_needed(M, N, K, 256) == 0 and L.jv_fp8_split_for(M, N, K, 256) == 1
 
 
+def test_batch_decode_plans_stay_within_their_bounds(product_lib):
+    """Over CU counts, weights and batch sizes: the batch-decode kernel runs
+    only at 17-128 tokens on K = 4096 / 12288 weights of at least 64 tiles,
+    with one workgroup per CU at most and half the CUs at least, 4 waves for
+    K = 4096 and 8 for K = 12288, and needs no K split, counters or partials."""
+    L = product_lib
+    seen = 0
+    for cus in (64, 80, 104, 120, 228, 256, 304):
+        for K in (2048, 4096, 8192, 12288):
+            for N in (256, 1008, 1024, 1040, 2048, 4096, 4112, 6144, 8192, 10240, 12288, 24576):
+                for M in (1, 16, 17, 31, 32, 33, 48, 50, 64, 65, 80, 96, 100, 112, 127, 128, 129, 256):
+                    kind, wgs, threads, splits = launch_shape(L, M, N, K, cus)
+                    if kind != 3:
+                        continue
+                    seen += 1
+                    assert 17 <= M <= 128 and K in (4096, 12288) and (N + 15) // 16 >= 64, (cus, M, N, K)
+                    assert wgs <= cus and 2 * wgs >= cus and splits == 1, (cus, M, N, K, wgs)
+                    assert threads == (256 if K == 4096 else 512), (cus, M, N, K)
+                    assert L.jv_fp8_split_for(M, N, K, cus) == 1 and L.jv_fp8_counters_needed(M, N, K, cus) == 0
+    assert seen > 100, seen
+
+
 def test_wide_weights_never_split_k(product_lib):
     """On weights wide enough for 1.5 rounds of 64-channel tiles the FP8 GEMM
     (from 17 tokens) and the W8A16 GEMM (from 32) leave the decode kernel at
