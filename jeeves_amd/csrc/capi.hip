@@ -290,6 +290,7 @@ int jv_fp8_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const 
 int64_t jv_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   const int cus = cu_count_of(-1);
   if (cus <= 0) return -1;
+  if (jv::w8a16_batch_plan(M, N, K, cus, nullptr)) return 0;
   return jv::w8a16_decode_kernel_for(M, N, cus) ? split_partial_bytes(M, N, K, cus) : 0;
 }
 
@@ -304,6 +305,11 @@ int jv_w8a16_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, cons
   const int cus = cu_count_of(-1);
   if (cus <= 0) return fail(JV_ERR_HIP, "cannot query the device's compute units");
   hipStream_t s = (hipStream_t)stream;
+  jv::BatchPlan batch;
+  if (jv::w8a16_batch_plan(M, N, K, cus, &batch))
+    return hip_status(jv::w8a16_batch((const uint16_t*)x, ldx, (const uint8_t*)w, ldw, (int)M, (int)N, (int)K, batch, w_scale,
+                                      (const uint16_t*)bias, (uint16_t*)y, ldy, s),
+                      "W8A16 batch GEMM launch");
   if (!jv::w8a16_decode_kernel_for(M, N, cus))
     return hip_status(jv::w8a16_prefill((const uint16_t*)x, ldx, (const uint8_t*)w, ldw, (int)M, (int)N, (int)K, w_scale,
                                         (const uint16_t*)bias, (uint16_t*)y, ldy, cus, s),

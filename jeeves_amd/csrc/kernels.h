@@ -136,6 +136,55 @@ inline bool batch_plan(int64_t M, int64_t N, int64_t K, int cu_count, bool swigl
   return true;
 }
 
+// The W8A16 parity mode's batch-decode plan (w8a16_batch_kernel, w8a16.hip):
+// the FP8 plan's waves and steps, with this mode's operand bytes: a workgroup
+// reads (rt + 2 mt) x 16 x K (bf16 activations), at most 6 such tiles and
+// 576 KiB, and holds at most 2 token tiles beside its weights. It is taken
+// only where it splits the batch's token tiles (msplit >= 2): unsplit, the
+// W8A16 decode kernel's eight waves keep more in flight (merged q/k/v at 32
+// tokens 12.4 vs 13.6 us). One round of workgroups; past 64 tokens, where
+// the alternative is the W8A16 prefill tiles, two rounds too. Measured on
+// MI355X (us, graphs over rotated weights, this plan vs the W8A16 decode
+// kernel or, past 64 tokens, its prefill tiles): k/v M = 32 / 64 / 128: 7.0 /
+// 6.9 / 7.7 vs 10.4 / 17.8 / 48.2; q/o M = 32 / 64 / 96 / 128: 8.9 / 12.8 /
+// 20.9 / 21.0 vs 10.9 / 18.4 / 48.5 / 48.7. Two rounds below 65 tokens lost
+// to the decode kernel (merged q/k/v 12.7 vs 10.2 us at 17, down 29.1 vs 19.8).
+inline int w8a16_batch_max_mt(int waves, int rt) { return waves == 4 ? 2 : (rt == 1 ? 1 : 0); }
+inline bool w8a16_batch_plan(int64_t M, int64_t N, int64_t K, int cu_count, BatchPlan* out) {
+  if (M < 17 || M > 128 || N <= 0 || cu_count <= 0) return false;
+  BatchPlan p{};
+  if (K == 32 * 128) {
+    p.waves = 4;
+    p.steps = 8;
+  } else if (K == 96 * 128) {
+    p.waves = 8;
+    p.steps = 12;
+  } else {
+    return false;
+  }
+  const int64_t tiles = (N + 15) / 16, mtall = (M + 15) / 16, cus = cu_count;
+  if (tiles < 64) return false;
+  int64_t best = 0;
+  for (int64_t rounds = 1; rounds <= (M > kDecodeMaxRows ? 2 : 1) && best == 0; ++rounds)
+    for (int rt = 1; rt <= 2; ++rt)
+      for (int64_t ms = 2; ms <= mtall; ++ms) {
+        if (mtall % ms) continue;
+        const int64_t mt = mtall / ms, groups = (tiles + rt - 1) / rt, cost = rt + 2 * mt, wgs = groups * ms;
+        if (mt > w8a16_batch_max_mt(p.waves, rt) || wgs > rounds * cus || 2 * wgs < rounds * cus) continue;
+        if (cost > 6 || cost * K > 36864) continue;
+        if (best == 0 || cost < best) {
+          best = cost;
+          p.rt = rt;
+          p.mt = (int)mt;
+          p.msplit = (int)ms;
+          p.groups = (int)groups;
+        }
+      }
+  if (best == 0) return false;
+  if (out) *out = p;
+  return true;
+}
+
 struct DecodePlan {
   int rt;      // 16-row tiles per wave
   int waves;   // waves per workgroup, splitting the workgroup's k range
@@ -251,6 +300,9 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
 hipError_t w8a16_decode(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
                         const DecodePlan& p, float* partial, int* counters, const float* sw, const uint16_t* bias,
                         uint16_t* y, int64_t ldy, hipStream_t stream);
+hipError_t w8a16_batch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                       const BatchPlan& p, const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy,
+                       hipStream_t stream);
 hipError_t w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
                          const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy, int cu_count,
                          hipStream_t stream);

@@ -11,6 +11,8 @@
 // the A side of v_mfma_f32_16x16x32_bf16, each wave streams its k range in
 // bursts straight from HBM, waves meet in LDS, narrow N splits K across
 // workgroups with the same deterministic last-workgroup reduction.
+#include <type_traits>
+
 #include "epilogue.h"
 #include "kernels.h"
 
@@ -203,6 +205,164 @@ __global__ __launch_bounds__(64 * W) void w8a16_decode_kernel(const uint16_t* __
     }
   }
   if (threadIdx.x == 0) __hip_atomic_store(counters + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Batch-decode form (17-128 tokens, w8a16_batch_plan): the FP8 batch-decode
+// kernel's structure (gemm_batch.hip) with this mode's operands -- each wave
+// issues its whole k range of e4m3 weight fragments at once, in step order,
+// the bf16 activation fragments stream two steps ahead, and workgroups split
+// the batch's token tiles (msplit parts per weight group, 8 workgroups apart
+// so the parts share an XCD's L2). Every output's k order is the decode
+// kernel's at the same waves per row (each wave's steps in order, the four
+// 32-deep MFMAs of a step in order, waves summed in order), so the two agree
+// bit for bit. Activations are the larger operand here (2 bytes per element
+// against 1): splitting the token tiles is what cuts each workgroup's reads.
+template <int I, int N, typename F>
+__device__ __forceinline__ void w8a16_each_step(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    w8a16_each_step<I + 1, N>(f);
+  }
+}
+
+template <int MT, int RT, int W, int NS, bool PACKW>
+__global__ __launch_bounds__(64 * W) void w8a16_batch_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                             const uint8_t* __restrict__ w, int64_t ldw, int M, int N,
+                                                             int K, int groups, int msplit, const float* __restrict__ sw,
+                                                             const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
+                                                             int64_t ldy) {
+  constexpr int D = 2;  // activation steps loaded ahead of the MFMAs
+  constexpr int WSTEP = PACKW ? 2048 : 128, WHALF = PACKW ? 1024 : 16;
+  __shared__ f32x4 red[W][RT * MT][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t b = blockIdx.x, ms = (uint32_t)msplit, whole = (uint32_t)groups & ~7u;
+  int group, mpart;
+  if (b < whole * ms) {
+    group = (int)((b / (8 * ms)) * 8 + (b & 7));
+    mpart = (int)((b >> 3) % ms);
+  } else {
+    const uint32_t r = (uint32_t)groups - whole, i = b - whole * ms;
+    group = (int)(whole + i % r);
+    mpart = (int)(i / r);
+  }
+  const int ksteps = K >> 7;
+  const int s_begin = wave * NS;
+  const int n0 = group * 16 * RT, mt0 = mpart * MT;
+  const int li = lane & 15, j32 = (lane >> 4) * 32;
+  const int ntiles = (N + 15) >> 4;
+  const uint8_t* wp[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+    wp[rt] = PACKW ? w + ((int64_t)min(group * RT + rt, ntiles - 1) * ksteps + s_begin) * 2048 + lane * 16
+                   : w + (int64_t)min(n0 + rt * 16 + li, N - 1) * ldw + j32 + s_begin * 128;
+  const uint16_t* xp[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xp[mt] = x + (int64_t)min((mt0 + mt) * 16 + li, M - 1) * ldx + j32 + s_begin * 128;
+
+  constexpr int kOut = RT * MT * 256, kThreads = 64 * W, kPer = (kOut + kThreads - 1) / kThreads;
+  float pre_sw[kPer], pre_b[kPer];
+  {
+    const uint16_t* bsrc = bias ? bias : reinterpret_cast<const uint16_t*>(sw);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int idx = min((int)threadIdx.x + j * kThreads, kOut - 1);
+      const int n = min(n0 + ((idx >> 8) / MT) * 16 + (idx & 15), N - 1);
+      pre_sw[j] = sw[n];
+      pre_b[j] = bf16_to_f32(bsrc[n]);
+    }
+  }
+  const bool has_bias = bias != nullptr;
+
+  i32x4 xa[D][MT][4];
+  auto load_x = [&](int u, i32x4 (&dst)[MT][4]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dst[mt][q] = *reinterpret_cast<const i32x4*>(xp[mt] + u * 128 + 8 * q);
+  };
+  w8a16_each_step<0, (D < NS ? D : NS)>([&](auto uc) { load_x(decltype(uc)::value, xa[decltype(uc)::value]); });
+  __builtin_amdgcn_sched_barrier(0);
+  i32x4 wa[NS][RT][2];
+  w8a16_each_step<0, NS>([&](auto uc) {
+    constexpr int u = decltype(uc)::value;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      wa[u][rt][0] = *reinterpret_cast<const i32x4*>(wp[rt] + u * WSTEP);
+      wa[u][rt][1] = *reinterpret_cast<const i32x4*>(wp[rt] + u * WSTEP + WHALF);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  f32x4 acc[RT][MT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  w8a16_each_step<0, NS>([&](auto uc) {
+    constexpr int u = decltype(uc)::value;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const i32x4 w0 = wa[u][rt][0], w1 = wa[u][rt][1];
+      const bf16x8 a[4] = {e4m3x8_to_bf16(w0.x, w0.y), e4m3x8_to_bf16(w0.z, w0.w), e4m3x8_to_bf16(w1.x, w1.y),
+                           e4m3x8_to_bf16(w1.z, w1.w)};
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[q], __builtin_bit_cast(bf16x8, xa[u % D][mt][q]),
+                                                                acc[rt][mt], 0, 0, 0);
+    }
+    if constexpr (u + D < NS) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_x(u + D, xa[u % D]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  });
+
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[wave][rt * MT + mt][lane] = acc[rt][mt];
+  __syncthreads();
+  const float* redf = reinterpret_cast<const float*>(&red[0][0][0]);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int idx = (int)threadIdx.x + j * kThreads;
+    if (kOut % kThreads != 0 && idx >= kOut) break;
+    const int t = idx >> 8, rt = t / MT, mt = t % MT, e = idx & 255, ml = e >> 4, nl = e & 15;
+    const int src = (t * 64 + ml + 16 * (nl >> 2)) * 4 + (nl & 3);
+    float sum = 0.0f;
+#pragma unroll
+    for (int wv = 0; wv < W; ++wv) sum += redf[wv * RT * MT * 256 + src];
+    const int m = (mt0 + mt) * 16 + ml, n = n0 + rt * 16 + nl;
+    if (m < M && n < N) y[(int64_t)m * ldy + n] = w8a16_out(sum, pre_sw[j], has_bias, pre_b[j]);
+  }
+}
+
+hipError_t w8a16_batch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
+                       const BatchPlan& p, const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy,
+                       hipStream_t stream) {
+  if (M < 1 || K / 128 != p.waves * p.steps || p.msplit < 1 || p.groups < 1 ||
+      (int64_t)p.mt * p.msplit != (M + 15) / 16 || p.mt > w8a16_batch_max_mt(p.waves, p.rt) ||
+      (int64_t)p.groups * p.rt * 16 < N)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(p.groups * p.msplit));
+#define JV_W8A16_BATCH_CASE(MT_, RT_, W_, NS_)                                                                      \
+  if (p.mt == MT_ && p.rt == RT_ && p.waves == W_ && p.steps == NS_) {                                           \
+    if (ldw == 0)                                                                                                 \
+      w8a16_batch_kernel<MT_, RT_, W_, NS_, true><<<grid, dim3(64 * W_), 0, stream>>>(x, ldx, w, ldw, M, N, K,     \
+                                                                                      p.groups, p.msplit, sw, bias, \
+                                                                                      y, ldy);                       \
+    else                                                                                                          \
+      w8a16_batch_kernel<MT_, RT_, W_, NS_, false><<<grid, dim3(64 * W_), 0, stream>>>(x, ldx, w, ldw, M, N, K,    \
+                                                                                       p.groups, p.msplit, sw,      \
+                                                                                       bias, y, ldy);               \
+    return hipGetLastError();                                                                                     \
+  }
+  JV_W8A16_BATCH_CASE(1, 1, 4, 8) JV_W8A16_BATCH_CASE(2, 1, 4, 8) JV_W8A16_BATCH_CASE(1, 2, 4, 8)
+  JV_W8A16_BATCH_CASE(2, 2, 4, 8) JV_W8A16_BATCH_CASE(1, 1, 8, 12)
+#undef JV_W8A16_BATCH_CASE
+  return hipErrorInvalidValue;
 }
 
 // Bursts of U steps: the operands of a burst (RT weight tiles, MT token tiles

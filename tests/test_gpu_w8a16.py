@@ -169,6 +169,35 @@ def test_w8a16_wide_small_batches_take_64x64_prefill_tiles(N):
         assert oracle.bitwise_equal_fraction(out, oracle.f64_to_bf16(exact)) >= EXACT_EQUAL_MIN, (N, M)
 
 
+# 17-128 tokens that take the W8A16 batch-decode plan: k/v (1024 x 4096),
+# q/o (4096 x 4096), a ragged 1040 channels; token counts whose last tile is
+# partly outside.
+@pytest.mark.parametrize("N,K,M", [(1024, 4096, 17), (1024, 4096, 48), (1024, 4096, 64), (1024, 4096, 80),
+                                   (1024, 4096, 128), (4096, 4096, 32), (4096, 4096, 64), (4096, 4096, 96),
+                                   (4096, 4096, 128), (1040, 4096, 40)])
+def test_w8a16_batch_decode(N, K, M):
+    """The batch-decode form: the reference's Metal acceptance (>= 99.9% equal
+    to the fp32 math, the float64 bound), every output bitwise equal to its
+    16-token slice on the W8A16 decode kernel (same waves per row), tiled
+    weights equal to row-major ones, the bias bitwise, no workspace."""
+    print(f"w8a16 batch N={N} K={K} M={M}", flush=True)
+    assert _lib.lib().jv_w8a16_workspace_bytes(M, N, K) == 0
+    g = torch.Generator().manual_seed(N + M)
+    wq, sw = quantize_rows((torch.randn(N, K, generator=g) * 0.02).cuda())
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    bias = (torch.randn(N, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    y = fp8_matmul_w8a16(x, wq, sw)
+    assert torch.equal(y, torch.cat([fp8_matmul_w8a16(x[i:i + 16], wq, sw) for i in range(0, M, 16)])), (N, M)
+    if N % 16 == 0:
+        assert torch.equal(fp8_matmul_w8a16(x, tile_weight(wq), sw, tiled=True), y), (N, M)
+    assert torch.equal(fp8_matmul_w8a16(x, wq, sw, bias=bias), y + bias), (N, M)
+    out = helpers.bits(y)
+    math = oracle.w8a16_math(helpers.bits(x), helpers.codes_np(wq), sw.cpu().numpy())
+    exact, magnitude = f64_parts(x, wq, sw)
+    assert oracle.bitwise_equal_fraction(out, math) >= MATH_EQUAL_MIN, (N, M)
+    assert oracle.within_metal_bound(oracle.bf16_to_f32(out), exact, magnitude * (BOUND_MAGNITUDE / 2.0 ** -20)), (N, M)
+
+
 @pytest.mark.parametrize("M", [16, 64, 256])
 def test_w8a16_every_code(M):
     """Every e4m3 code through the in-kernel widening: weight row n holds code
