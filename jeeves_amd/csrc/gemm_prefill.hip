@@ -994,6 +994,12 @@ hipError_t w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64
   // four stages deep (gate+up at 32 tokens 31.3 us; three stages 34.5, six
   // 34.7: each stage holds only 4 KB of weight).
   if (M <= kDecodeMaxRows) return launch_w8a16_prefill<64, 64, 2, 2, 4>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 8, stream);
+  // Also where 128x128 tiles would not fill one round of CUs (q/o at 96
+  // tokens: 32 of them), except on the wide weights above: the 64x64 tiles
+  // give four times the workgroups.
+  const int64_t t128sq = ((int64_t)(M + 127) / 128) * ((N + 127) / 128);
+  if (t128sq < (int64_t)cu_count && 2 * ((N + 63) / 64) < 3 * (int64_t)cu_count)
+    return launch_w8a16_prefill<64, 64, 2, 2, 4>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 8, stream);
   const int64_t t256 = ((int64_t)(M + 255) / 256) * ((N + 255) / 256);
   if (t256 >= 2 * (int64_t)cu_count)
     return launch_w8a16_prefill<256, 256, 2, 4, 3>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 4, stream);
