@@ -1126,28 +1126,35 @@ static hipError_t launch_prefill_pp(const uint8_t* xq, int64_t ldx, const uint8_
 }
 
 // Time model of a lockstep launch, fitted (least squares on log time) to
-// 423 timings on MI355X of the three lockstep tiles at 1-8 K splits over the
-// 9B projection shapes (q/o, k/v, merged q/k/v, gate+up, down) at M = 65-1536.
+// 965 timings on MI355X of the five lockstep tiles at 1-8 K splits (graphs
+// of back-to-back launches over rotated weights) over 16 weights: N = 1024,
+// 4096, 6144, 8192, 10240, 12288, 24576 at K = 4096 (the 9B projections and
+// merged widths), 1024-4096 at K = 2048, 8192 and 12288 (down), at M =
+// 160-2048.
 // Workgroups run in rounds of cu_count * per_cu. Per 4096 of K a workgroup
 // takes `light` us in a round with few workgroups and `full` us in a full one
 // (HBM, L2 and LDS bandwidth shared), plus `item` us of prologue and
 // epilogue; a split launch adds the partial write, the count and the last
 // workgroup's loads, growing with the partial tile bytes and the rounds. The
-// argmin of the model is within 1.5% of the fastest measured choice summed
-// over those shapes (the fixed tile rules it replaces: 20%).
+// argmin of the model is within 0.3% of the fastest measured choice summed
+// over those shapes; the three tiles without the 5-stage ones: 2.9% (q/o at
+// 512 tokens 18.5 -> 15.9 us, k/v at 2048 17.7 -> 15.4, merged q/k/v at 256
+// 19.0 -> 16.6).
 struct LockstepCost {
   PrefillTile tile;
   int per_cu;         // workgroups per CU (LDS and VGPR occupancy)
   double light, full, item;
 };
 static const LockstepCost kLockstepCosts[] = {
-    {{256, 128, 2, 4, 128, 3, 4}, 1, 27.28, 37.26, 5.03},
-    {{128, 128, 2, 2, 128, 4, 8}, 1, 16.30, 19.58, 4.48},
-    {{64, 64, 2, 2, 128, 4, 8}, 2, 10.48, 16.23, 1.08},
+    {{256, 128, 2, 4, 128, 3, 4}, 1, 30.22, 34.48, 3.97},
+    {{128, 128, 2, 2, 128, 4, 8}, 1, 15.08, 18.21, 5.58},
+    {{64, 128, 2, 4, 128, 5, 8}, 1, 11.69, 12.83, 2.46},
+    {{64, 64, 2, 2, 128, 5, 8}, 1, 8.66, 8.33, 2.37},
+    {{64, 64, 2, 2, 128, 4, 8}, 2, 8.66, 15.29, 2.45},
 };
 // A split launch: a fixed cost, a cost per split, and a cost per split of a
 // 128x128 fp32 partial per round.
-constexpr double kSplitBaseUs = 3.63, kSplitEachUs = 0.49, kSplitPerTileUs = 0.40;
+constexpr double kSplitBaseUs = 2.51, kSplitEachUs = 0.16, kSplitPerTileUs = 0.81;
 
 static double lockstep_time_us(const LockstepCost& c, int64_t M, int64_t N, int64_t K, int splits, int cu_count) {
   const int64_t tiles = ((M + c.tile.bm - 1) / c.tile.bm) * ((N + c.tile.bn - 1) / c.tile.bn);

@@ -98,13 +98,13 @@ def test_split_for_is_pure_host_logic(product_lib):
     assert L.jv_fp8_split_for(31, 4096, 12288, 256) == 1    # below 32 tokens: the batch-decode kernel
     # above 128 tokens: the lockstep tile and K split of least modelled time; a
     # split keeps at least four 128-deep stages, at most 8
-    assert L.jv_fp8_split_for(256, 4096, 12288, 256) == 4   # 64 tiles of 128x128
-    assert L.jv_fp8_counters_needed(256, 4096, 12288, 256) == 64
+    assert L.jv_fp8_split_for(256, 4096, 12288, 256) == 2   # 128 tiles of 64x128
+    assert L.jv_fp8_counters_needed(256, 4096, 12288, 256) == 128
     assert L.jv_fp8_split_for(512, 4096, 12288, 256) == 2   # 128 tiles of 128x128
     assert L.jv_fp8_split_for(128, 1024, 8192, 256) == 4    # 32 tiles
     assert L.jv_fp8_split_for(256, 1024, 512, 256) == 1     # 4 stages of 128 leave no room to split
-    assert L.jv_fp8_split_for(512, 1024, 4096, 256) == 4    # 128 tiles
-    assert L.jv_fp8_split_for(512, 4096, 4096, 256) == 1    # 512 tiles fill the CUs
+    assert L.jv_fp8_split_for(512, 1024, 4096, 256) == 2    # 128 tiles of 64x64
+    assert L.jv_fp8_split_for(512, 4096, 4096, 256) == 1    # 256 tiles of 64x128 fill the CUs
     assert L.jv_fp8_split_for(1040, 2048, 4096, 256) == 1
     assert L.jv_fp8_split_for(2048, 4096, 4096, 256) == 1   # 256x128 tiles
     assert L.jv_fp8_counters_needed(2048, 4096, 4096, 256) == 0
