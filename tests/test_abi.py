@@ -168,6 +168,29 @@ def test_batch_decode_plans_stay_within_their_bounds(product_lib):
     assert seen > 100, seen
 
 
+def test_lockstep_model_picks_the_measured_fastest_tiles(product_lib):
+    """Above 128 tokens the lockstep tile of least modelled time: the 5-stage
+    64x128 / 64x64 rings where one round of small tiles is bound by the bytes
+    each CU keeps in flight (q/o at 256-512 tokens, k/v at 768-2048), 128x128
+    and 256x128 where whole rounds of larger tiles fit; the fastest choices
+    in alternating A/B timings on MI355X (256 CUs). Workgroups and threads
+    name the tile: 64x64 runs 4 waves, 64x128 and 256x128 run 8."""
+    L = product_lib
+    # (M, N, K): (workgroups, threads, splits)
+    want = {(256, 4096, 4096): (256, 256, 1),     # 64x64, 5 stages: 12.2 us vs 14.7 on 64x64 split 2
+            (512, 4096, 4096): (256, 512, 1),     # 64x128, 5 stages: 16.2 vs 18.6 on 64x64
+            (512, 1024, 4096): (256, 256, 2),     # 64x64, 5 stages, 2 splits: 10.1 vs 11.0
+            (1024, 1024, 4096): (256, 256, 1),    # 64x64, 5 stages: 11.7 vs 13.4
+            (2048, 1024, 4096): (256, 512, 1),    # 64x128, 5 stages: 15.7 vs 17.6
+            (256, 8192, 4096): (256, 512, 1),     # 64x128, 5 stages: 17.5 vs 20.4
+            (1024, 4096, 4096): (256, 256, 1),    # 128x128
+            (2048, 4096, 4096): (256, 512, 1),    # 256x128
+            (512, 4096, 12288): (256, 256, 2)}    # 128x128, 2 splits
+    for (M, N, K), (wgs, threads, splits) in want.items():
+        kind, got_wgs, got_threads, got_splits = launch_shape(L, M, N, K)
+        assert (kind, got_wgs, got_threads, got_splits) == (1, wgs, threads, splits), (M, N, K)
+
+
 def test_wide_weights_never_split_k(product_lib):
     """On weights wide enough for 1.5 rounds of 64-channel tiles the FP8 GEMM
     (from 17 tokens) and the W8A16 GEMM (from 32) leave the decode kernel at
