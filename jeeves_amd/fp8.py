@@ -41,8 +41,8 @@ QUANT_MAX_PACKED_COLS = 16384
 BLOCK_K = 128
 TILE_COUNTER_SLOTS = 1 << 16
 # One row count per kernel variant: 1-4 decode token tiles, then prefill
-# batches that select the 256x256, 256x128, 128x128 and 64x64 tiles on large and
-# small N (inference/fp8.py:32 plays the same role for Triton's JIT).
+# batches that select the 256x256, 256x128, 128x128, 64x128 and 64x64 tiles on
+# large and small N (inference/fp8.py:32 plays the same role for Triton's JIT).
 WARM_ROWS = (1, 16, 17, 32, 33, 48, 49, 64, 65, 256, 300, 2048)
 LORA_RANKS = (16,)
 
