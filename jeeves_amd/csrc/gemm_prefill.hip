@@ -1221,14 +1221,20 @@ PrefillTile prefill_tile(int64_t M, int64_t N, int64_t K, int cu_count, bool spl
   if (t256 * 8 >= cus * 5) return PrefillTile{256, 256, 2, 4, 64, 4, 4, true};
   // Else the lockstep tile and K split of least modelled time; each split
   // keeps at least four BK-deep stages and the partials at most
-  // kMaxPrefillPartialBytes.
+  // kMaxPrefillPartialBytes, and a split fills at most one round of
+  // workgroups (splits that spill into a second round measured slower than
+  // the model puts them: down at M = 320 34.2 us on 128x128 tiles with 2
+  // splits against 37.9 on 64x128 with 3).
   PrefillTile best{64, 64, 2, 2, 128, 4, 8};
   double best_us = 1e300;
   for (const LockstepCost& c : kLockstepCosts) {
+    const int64_t tiles = ((M + c.tile.bm - 1) / c.tile.bm) * ((N + c.tile.bn - 1) / c.tile.bn);
     for (int s = 1; s <= (split_k ? kMaxPrefillSplits : 1); ++s) {
       PrefillTile t = c.tile;
       t.splits = s;
-      if (s > 1 && (K / t.bk < 4 * s || prefill_partial_bytes(t, M, N) > kMaxPrefillPartialBytes)) break;
+      if (s > 1 && (K / t.bk < 4 * s || prefill_partial_bytes(t, M, N) > kMaxPrefillPartialBytes ||
+                    tiles * s > cus * c.per_cu))
+        break;
       const double us = lockstep_time_us(c, M, N, K, s, cu_count);
       if (us < best_us) best_us = us, best = t;
     }
