@@ -139,12 +139,22 @@ __device__ __forceinline__ f32x16 lora_block(i32x4 b, const float4 (&t)[2]) {
   return l;
 }
 
+// XOR swizzle span of an LDS-staged output tile row of W 16-byte chunks: the
+// largest power of two up to 32 dividing W, so chunk ^ (row % span) stays in
+// the row (W itself for the power-of-two widths).
+template <int W>
+constexpr int out_swizzle() {
+  int s = 1;
+  while (s < 32 && W % (2 * s) == 0) s *= 2;
+  return s;
+}
+
 // Epilogue of both FP8 prefill kernels. 32x32 MFMA output layout: lane l
 // holds column l % 32 (a token) and, in register r, row 8*(r/4) + 4*(l/32) +
 // r%4 (a channel): each register quad is 4 consecutive channels of one token.
 // y = bf16((acc * sx[m]) * sw[n] (+ lora_scale * l[n, m])), then + bias[n] in bf16. The
 // finished bf16 tile goes through LDS ([BM tokens][BN channels], 16-byte
-// chunk c of row r stored at chunk c ^ (r % OUT_CH)) so that global stores are
+// chunk c of row r stored at chunk c ^ (r % out_swizzle)) so that global stores are
 // 16 bytes per lane over whole row segments. The caller's operand reads and
 // copies into `lds` are complete (this wave's) when it is called.
 template <int BM, int BN, int WGM, int WGN, int RANK>
@@ -155,7 +165,7 @@ __device__ __forceinline__ void store_tile(uint8_t* lds, const float* scale_lds,
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int OUT_CH = BN * 2 / 16;  // 16-byte chunks per output tile row
-  static_assert(OUT_CH <= 32 && (OUT_CH & (OUT_CH - 1)) == 0, "output tile width");
+  constexpr int SWZ = out_swizzle<OUT_CH>();
   static_assert(RANK == 0 || RANK == 16, "LoRA rank");
   LoraOperands<TN, TM> lo;
   if constexpr (RANK > 0) load_lora(lo, ep, n0 + wn * WN, m0 + wm * WM, M, N, lane);
@@ -185,7 +195,7 @@ __device__ __forceinline__ void store_tile(uint8_t* lds, const float* scale_lds,
           if constexpr (RANK > 0) v[e] += lora[4 * q + e] * ep.lora_scale;
           if (ep.bias) v[e] = with_bias(ep, v[e], bf16_to_f32(ep.bias[min(n + e, N - 1)]));
         }
-        const int chunk = (nl >> 3) ^ (ml % OUT_CH);
+        const int chunk = (nl >> 3) ^ (ml % SWZ);
         *reinterpret_cast<uint2*>(lds + ml * (BN * 2) + chunk * 16 + (nl & 4) * 2) =
             uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
       }
@@ -199,7 +209,7 @@ __device__ __forceinline__ void store_tile(uint8_t* lds, const float* scale_lds,
     const int ml = c / OUT_CH, ch = c % OUT_CH;
     const int m = m0 + ml, n = n0 + ch * 8;
     if (m >= M || n >= N) continue;
-    const uint4 v = *reinterpret_cast<const uint4*>(lds + ml * (BN * 2) + (ch ^ (ml % OUT_CH)) * 16);
+    const uint4 v = *reinterpret_cast<const uint4*>(lds + ml * (BN * 2) + (ch ^ (ml % SWZ)) * 16);
     uint16_t* dst = ep.y + (int64_t)m * ep.ldy + n;
     if (y_vec) {
       *reinterpret_cast<uint4*>(dst) = v;
@@ -230,7 +240,7 @@ __device__ __forceinline__ void store_tile_sw(uint8_t* lds, const float* scale_l
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int HBN = BN / 2;               // h channels per tile
   constexpr int OUT_CH = HBN * 2 / 16;      // 16-byte chunks per h tile row
-  static_assert(OUT_CH <= 32 && (OUT_CH & (OUT_CH - 1)) == 0, "output tile width");
+  constexpr int SWZ = out_swizzle<OUT_CH>();
   static_assert(RANK == 0 || RANK == 16, "LoRA rank");
   LoraOperands<TN, TM> lo;
   if constexpr (RANK > 0) load_lora(lo, ep, n0 + wn * WN, m0 + wm * WM, M, N, lane);
@@ -274,7 +284,7 @@ __device__ __forceinline__ void store_tile_sw(uint8_t* lds, const float* scale_l
         if (ep.parts)
           mx = max(max(mx, max(h01 & 0x7FFFu, (h01 >> 16) & 0x7FFFu)), max(h23 & 0x7FFFu, (h23 >> 16) & 0x7FFFu));
         const int hl = cb / 2 + o;  // h channel within the tile
-        const int chunk = (hl >> 3) ^ (ml % OUT_CH);
+        const int chunk = (hl >> 3) ^ (ml % SWZ);
         *reinterpret_cast<uint2*>(lds + ml * (HBN * 2) + chunk * 16 + (hl & 4) * 2) = uint2{h01, h23};
       }
       if (ep.parts) {
@@ -295,7 +305,7 @@ __device__ __forceinline__ void store_tile_sw(uint8_t* lds, const float* scale_l
     const int m = m0 + ml;
     const int64_t hn = h0 + ch * 8;
     if (m >= M || hn >= ep.half) continue;
-    const uint4 v = *reinterpret_cast<const uint4*>(lds + ml * (HBN * 2) + (ch ^ (ml % OUT_CH)) * 16);
+    const uint4 v = *reinterpret_cast<const uint4*>(lds + ml * (HBN * 2) + (ch ^ (ml % SWZ)) * 16);
     uint16_t* dst = ep.y + (int64_t)m * ep.ldy + hn;
     if (y_vec) {
       *reinterpret_cast<uint4*>(dst) = v;
@@ -1125,27 +1135,31 @@ static hipError_t launch_prefill_pp(const uint8_t* xq, int64_t ldx, const uint8_
   return hipGetLastError();
 }
 
-// Time model of a lockstep launch, fitted (least squares on log time) to
-// 965 timings on MI355X of the five lockstep tiles at 1-8 K splits (graphs
-// of back-to-back launches over rotated weights) over 16 weights: N = 1024,
-// 4096, 6144, 8192, 10240, 12288, 24576 at K = 4096 (the 9B projections and
-// merged widths), 1024-4096 at K = 2048, 8192 and 12288 (down), at M =
-// 160-2048.
+// Time model of a prefill launch, fitted (least squares on log time) to
+// timings on MI355X (graphs of back-to-back launches over rotated weights):
+// the five lockstep tiles at 1-8 K splits, 965 timings over 16 weights (N =
+// 1024, 4096, 6144, 8192, 10240, 12288, 24576 at K = 4096, the 9B projections
+// and merged widths; 1024-4096 at K = 2048, 8192 and 12288) at M = 160-2048;
+// the two ping-pong tiles (no K split), 128 timings over 8 of those weights at
+// M = 256-4096.
 // Workgroups run in rounds of cu_count * per_cu. Per 4096 of K a workgroup
 // takes `light` us in a round with few workgroups and `full` us in a full one
 // (HBM, L2 and LDS bandwidth shared), plus `item` us of prologue and
 // epilogue; a split launch adds the partial write, the count and the last
 // workgroup's loads, growing with the partial tile bytes and the rounds. The
-// argmin of the model is within 0.3% of the fastest measured choice summed
-// over those shapes; the three tiles without the 5-stage ones: 2.9% (q/o at
-// 512 tokens 18.5 -> 15.9 us, k/v at 2048 17.7 -> 15.4, merged q/k/v at 256
-// 19.0 -> 16.6).
-struct LockstepCost {
+// argmin of the model is within 0.2% of the fastest measured choice summed
+// over those shapes; the lockstep tiles alone with 256x256 ping-pong tiles
+// from five eighths of a round: 1.5% (merged q/k/v at M = 1536 61.9 -> 43.9
+// us, the 12288-wide merge at M = 768 63.1 -> 44.8, gate+up at M = 768 96.3 ->
+// 88.4, merged q/k/v at M = 3072 91.4 -> 81.2).
+struct TileCost {
   PrefillTile tile;
   int per_cu;         // workgroups per CU (LDS and VGPR occupancy)
   double light, full, item;
 };
-static const LockstepCost kLockstepCosts[] = {
+static const TileCost kTileCosts[] = {
+    {{256, 256, 2, 4, 64, 4, 4, true}, 1, 29.60, 42.54, 9.98},
+    {{128, 384, 2, 4, 64, 4, 8, true}, 1, 30.21, 37.16, 8.92},
     {{256, 128, 2, 4, 128, 3, 4}, 1, 30.22, 34.48, 3.97},
     {{128, 128, 2, 2, 128, 4, 8}, 1, 15.08, 18.21, 5.58},
     {{64, 128, 2, 4, 128, 5, 8}, 1, 11.69, 12.83, 2.46},
@@ -1156,7 +1170,7 @@ static const LockstepCost kLockstepCosts[] = {
 // 128x128 fp32 partial per round.
 constexpr double kSplitBaseUs = 2.51, kSplitEachUs = 0.16, kSplitPerTileUs = 0.81;
 
-static double lockstep_time_us(const LockstepCost& c, int64_t M, int64_t N, int64_t K, int splits, int cu_count) {
+static double tile_time_us(const TileCost& c, int64_t M, int64_t N, int64_t K, int splits, int cu_count) {
   const int64_t tiles = ((M + c.tile.bm - 1) / c.tile.bm) * ((N + c.tile.bn - 1) / c.tile.bn);
   const int64_t items = tiles * splits, slots = (int64_t)cu_count * c.per_cu;
   const int64_t rounds = items / slots, rest = items % slots;
@@ -1212,30 +1226,30 @@ static bool small_batch_tile(int64_t M, int64_t N, int64_t K, int64_t cus, bool 
 PrefillTile prefill_tile(int64_t M, int64_t N, int64_t K, int cu_count, bool split_k) {
   PrefillTile small;
   if (M <= 2 * kDecodeMaxRows && small_batch_tile(M, N, K, cu_count, split_k, small)) return small;
-  // 256x256 tiles in the ping-pong form (least L2 -> LDS traffic per flop,
-  // and the fastest tile per CU) once they cover five eighths of the CUs,
-  // even in a partial round: gate+up at M = 512 (192 tiles) 52.7 us against
-  // 72 us with 128x128 and 74 us with 256x128.
+  // From five eighths of a round of 256x256 tiles on, the ping-pong tiles
+  // (least L2 -> LDS traffic per flop, the fastest tiles per CU) only: the
+  // model's lockstep terms were fitted up to M = 2048. Else every tile.
   const int64_t cus = cu_count;
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-  if (t256 * 8 >= cus * 5) return PrefillTile{256, 256, 2, 4, 64, 4, 4, true};
-  // Else the lockstep tile and K split of least modelled time; each split
-  // keeps at least four BK-deep stages and the partials at most
-  // kMaxPrefillPartialBytes, and a split fills at most one round of
-  // workgroups (splits that spill into a second round measured slower than
-  // the model puts them: down at M = 320 34.2 us on 128x128 tiles with 2
-  // splits against 37.9 on 64x128 with 3).
+  const bool pingpong_only = t256 * 8 >= cus * 5;
+  // The tile and K split of least modelled time (ping-pong tiles keep whole
+  // k ranges); each split keeps at least four BK-deep stages and the
+  // partials at most kMaxPrefillPartialBytes, and a split fills at most one
+  // round of workgroups (splits that spill into a second round measured
+  // slower than the model puts them: down at M = 320 34.2 us on 128x128
+  // tiles with 2 splits against 37.9 on 64x128 with 3).
   PrefillTile best{64, 64, 2, 2, 128, 4, 8};
   double best_us = 1e300;
-  for (const LockstepCost& c : kLockstepCosts) {
+  for (const TileCost& c : kTileCosts) {
+    if (pingpong_only && !c.tile.pingpong) continue;
     const int64_t tiles = ((M + c.tile.bm - 1) / c.tile.bm) * ((N + c.tile.bn - 1) / c.tile.bn);
-    for (int s = 1; s <= (split_k ? kMaxPrefillSplits : 1); ++s) {
+    for (int s = 1; s <= (split_k && !c.tile.pingpong ? kMaxPrefillSplits : 1); ++s) {
       PrefillTile t = c.tile;
       t.splits = s;
       if (s > 1 && (K / t.bk < 4 * s || prefill_partial_bytes(t, M, N) > kMaxPrefillPartialBytes ||
                     tiles * s > cus * c.per_cu))
         break;
-      const double us = lockstep_time_us(c, M, N, K, s, cu_count);
+      const double us = tile_time_us(c, M, N, K, s, cu_count);
       if (us < best_us) best_us = us, best = t;
     }
   }
@@ -1257,6 +1271,7 @@ hipError_t gemm_prefill(const uint8_t* xq, int64_t ldx, const uint8_t* w, int64_
   if (t.bm == BM_ && t.bn == BN_ && t.stages == ST_) \
     return launch_prefill_pp<BM_, BN_, ST_>(xq, ldx, w, ldw, M, N, K, ep, rank, t.group_m, stream);
     JV_PREFILL_PP_CASE(256, 256, 4)
+    JV_PREFILL_PP_CASE(128, 384, 4)
 #undef JV_PREFILL_PP_CASE
     return hipErrorInvalidValue;
   }
