@@ -221,6 +221,12 @@ static hipError_t launch_rows(int shape, const uint16_t* x, int64_t ldx, const u
                               uint8_t* codes, int64_t ldc, float* scales, uint16_t* h_out, int64_t ldh,
                               const uint16_t* lora_a, float* lora_t, hipStream_t stream) {
   if (M > kDecodeMaxRows) shape = quant_wide_shape(K);
+  // Long batches of long rows (h of the down projection in prefill): 1024
+  // threads x 2 chunks, more bytes in flight per row (graphs of back-to-back
+  // launches, K = 12288: 241 vs 269 us at M = 30801, 65.2 vs 67.4 at 8192;
+  // at 2048 the 256-thread shape stays ahead, 15.3 vs 15.5). Without LoRA, so
+  // t keeps its summation order.
+  if (RANK == 0 && K > 8192 && M >= 4096) shape = 3;
   if (PACKED && M > kDecodeMaxRows)
     return launch_rows_grid<SWIGLU, RANK, PACKED, true>(shape, x, ldx, up, ldu, M, K, codes, ldc, scales, h_out, ldh, lora_a,
                                                         lora_t, stream);

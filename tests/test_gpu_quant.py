@@ -61,9 +61,10 @@ def test_every_row_length(K):
 
 # Packed codes of prefill batches (the rows of a 16-token tile on one XCD):
 # every row length class, special rows (huge, zero, inf, NaN, tiny) spread
-# over the tiles, a partial last tile, and the prefill step's shapes.
+# over the tiles, a partial last tile, the prefill step's shapes, and a long
+# batch of long rows (1024-thread workgroups).
 @pytest.mark.parametrize("M, K", [(M, K) for M in (65, 200) for K in (128, 1024, 2048, 4096, 6144, 12288, 16384)]
-                         + [(2048, 4096), (2048, 12288), (1000, 8192)])
+                         + [(2048, 4096), (2048, 12288), (1000, 8192), (4100, 12288)])
 def test_packed_prefill_rows(M, K):
     from jeeves_amd.fp8 import packed_codes_bytes, tile_weight
 
