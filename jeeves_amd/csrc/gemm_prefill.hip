@@ -1010,11 +1010,26 @@ hipError_t w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64
   const int64_t t128sq = ((int64_t)(M + 127) / 128) * ((N + 127) / 128);
   if (t128sq < (int64_t)cu_count && 2 * ((N + 63) / 64) < 3 * (int64_t)cu_count)
     return launch_w8a16_prefill<64, 64, 2, 2, 4>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 8, stream);
+  // From five eighths of a round of 256x256 tiles on, 256x256 or 256x128
+  // tiles, whichever needs less time in whole rounds: a round of 256x256
+  // tiles takes 1.65 times one of 256x128 (123 / 73 us full at K = 4096, 101 /
+  // 63 alone). Merged q/k/v at M = 2048 106.8 us on 256x256 tiles against
+  // 132.4 on 256x128, gate+up at M = 512 110.0 against 133.8, the 10240-wide
+  // merge at M = 1024 104.0 against 131.2, q/o and down at M = 4096 120.5 /
+  // 350.9 against 148.8 / 414.3; 256x128 where the 256x256 tiles spill into a
+  // part-filled round: gate+up at M = 768 202.3 against 216.7, the
+  // 10240-wide merge at M = 2048 202.8 against 216.0. Below that 256x128
+  // from a round of them, else 128x128 (us, graphs over rotated weights).
+  const int64_t cus = cu_count;
   const int64_t t256 = ((int64_t)(M + 255) / 256) * ((N + 255) / 256);
-  if (t256 >= 2 * (int64_t)cu_count)
-    return launch_w8a16_prefill<256, 256, 2, 4, 3>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 4, stream);
   const int64_t t128 = ((int64_t)(M + 255) / 256) * ((N + 127) / 128);
-  if (t128 >= cu_count)
+  if (t256 * 8 >= 5 * cus) {
+    const int64_t r256 = (t256 + cus - 1) / cus, r128 = (t128 + cus - 1) / cus;
+    if (33 * r256 <= 20 * r128)
+      return launch_w8a16_prefill<256, 256, 2, 4, 3>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 4, stream);
+    return launch_w8a16_prefill<256, 128, 2, 4, 3>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 4, stream);
+  }
+  if (t128 >= cus)
     return launch_w8a16_prefill<256, 128, 2, 4, 3>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 4, stream);
   return launch_w8a16_prefill<128, 128, 2, 2, 3>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 8, stream);
 }
