@@ -143,8 +143,10 @@ int jv_fp8_linear_noalloc(const void* x, int64_t ldx, const void* w, int64_t ldw
  *   then, with a bias, y[m,n] = bf16( y[m,n] + bias[n] ).
  * No activation quantization: the bf16 activations enter the GEMM as they
  * are. Arguments as jv_fp8_linear (no LoRA); K a positive multiple of 128.
- * workspace: jv_w8a16_workspace_bytes(M,N,K) bytes (split-K partials, 0 for
- * most shapes); tile_counters as jv_fp8_linear. */
+ * workspace: jv_w8a16_workspace_bytes(M,N,K) bytes (split-K partials of the
+ * decode kernel or of the prefill kernel's 64x64 tiles, 0 for most shapes);
+ * tile_counters as jv_fp8_linear, needed whenever that size is not 0 (the
+ * call checks that the split's tiles fit n_counters). */
 int64_t jv_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int jv_w8a16_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
                     void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,

@@ -291,7 +291,8 @@ int64_t jv_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   const int cus = cu_count_of(-1);
   if (cus <= 0) return -1;
   if (jv::w8a16_batch_plan(M, N, K, cus, nullptr)) return 0;
-  return jv::w8a16_decode_kernel_for(M, N, cus) ? split_partial_bytes(M, N, K, cus) : 0;
+  if (jv::w8a16_decode_kernel_for(M, N, cus)) return split_partial_bytes(M, N, K, cus);
+  return round_up(jv::w8a16_prefill_partial_bytes(M, N, K, cus), 256);
 }
 
 int jv_w8a16_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const float* w_scale, const void* bias,
@@ -310,10 +311,23 @@ int jv_w8a16_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, cons
     return hip_status(jv::w8a16_batch((const uint16_t*)x, ldx, (const uint8_t*)w, ldw, (int)M, (int)N, (int)K, batch, w_scale,
                                       (const uint16_t*)bias, (uint16_t*)y, ldy, s),
                       "W8A16 batch GEMM launch");
-  if (!jv::w8a16_decode_kernel_for(M, N, cus))
+  if (!jv::w8a16_decode_kernel_for(M, N, cus)) {
+    const int splits = jv::w8a16_prefill_splits(M, N, K, cus);
+    float* partials = nullptr;
+    if (splits > 1) {
+      const int64_t tiles = jv::w8a16_prefill_counters(M, N, K, cus);
+      if (!tile_counters || tiles > n_counters)
+        return fail(JV_ERR_VALUE, "%lld tiles exceed the %lld tile counters", (long long)tiles, (long long)n_counters);
+      const int64_t need = jv::w8a16_prefill_partial_bytes(M, N, K, cus);
+      if (!workspace || workspace_bytes < need)
+        return fail(JV_ERR_VALUE, "workspace too small for split-K partials: %lld < %lld bytes", (long long)workspace_bytes,
+                    (long long)need);
+      partials = reinterpret_cast<float*>(workspace);
+    }
     return hip_status(jv::w8a16_prefill((const uint16_t*)x, ldx, (const uint8_t*)w, ldw, (int)M, (int)N, (int)K, w_scale,
-                                        (const uint16_t*)bias, (uint16_t*)y, ldy, cus, s),
+                                        (const uint16_t*)bias, (uint16_t*)y, ldy, splits, partials, tile_counters, cus, s),
                       "W8A16 prefill GEMM launch");
+  }
   const jv::DecodePlan plan = jv::decode_plan(M, N, K, cus);
   float* partial = nullptr;
   if (plan.splits > 1) {

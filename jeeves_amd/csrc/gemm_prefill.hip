@@ -816,11 +816,11 @@ __global__ __launch_bounds__(512) void gemm_prefill_pp_kernel(const uint8_t* __r
 // lane half h of the 32x32 operand layout covers k = 32h + [0, 32) of the
 // stage; MFMA q of the stage uses k = 32h + 8q + [0, 8) on both operands.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int WGM, int WGN, int STAGES, bool PACKW>
+template <int BM, int BN, int WGM, int WGN, int STAGES, bool PACKW, bool SPLITK = false>
 __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_prefill_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw, int M, int N, int K,
     int tiles_m, int tiles_n, int group_m, const float* __restrict__ sw, const uint16_t* __restrict__ bias,
-    uint16_t* __restrict__ y, int64_t ldy) {
+    uint16_t* __restrict__ y, int64_t ldy, int splits, float* __restrict__ partials, int* __restrict__ counters) {
   constexpr int NW = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -832,9 +832,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_prefill_kernel(
   static_assert(XBYTES % (1024 * NW) == 0 && (BN * WROW) % (1024 * NW) == 0 && TM >= 1 && TN >= 1, "tile shape");
   static_assert(STAGES >= 2 && (STAGES - 2) * (XLOADS + WLOADS) < 64, "pipeline depth");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+  __shared__ int is_last;
 
+  // With a K split, workgroup tile + s * tiles adds up part s of the k range
+  // (whole 64-deep stages) and the last of a tile's workgroups to count in
+  // sums the parts in split order and runs the epilogue (split_k_reduce).
+  const int tiles = tiles_m * tiles_n;
+  const int split = SPLITK ? (int)blockIdx.x / tiles : 0;
+  const int tile = (int)blockIdx.x - split * tiles;
   int tile_m, tile_n;
-  tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tile_m, tile_n);
+  tile_of(tile, tiles_m, tiles_n, group_m, tile_m, tile_n);
   const int m0 = tile_m * BM, n0 = tile_n * BN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
@@ -856,11 +863,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_prefill_kernel(
     wsrc[i] = PACKW ? w + tiled_w_offset(min(n0 + r, N - 1), chunk * 16, K >> 7)
                     : w + (int64_t)min(n0 + r, N - 1) * ldw + chunk * 16;
   }
+  // This workgroup's stages: [kt0, kt0 + KT) of the K / 64 stages.
+  const int kt_all = K / 64;
+  int kt0 = 0, KT = kt_all;
+  if constexpr (SPLITK) {
+    kt0 = (int)((uint32_t)(kt_all * split) / (uint32_t)splits);
+    KT = (int)((uint32_t)(kt_all * (split + 1)) / (uint32_t)splits) - kt0;
+  }
   auto issue_stage = [&](int kt) {
     uint8_t* base = lds + (kt % STAGES) * STAGE;
-    const int64_t wk = PACKW ? tiled_stage_offset<64>(kt) : (int64_t)kt * 64;
+    const int ktg = kt0 + kt;
+    const int64_t wk = PACKW ? tiled_stage_offset<64>(ktg) : (int64_t)ktg * 64;
 #pragma unroll
-    for (int i = 0; i < XLOADS; ++i) load_lds16(xsrc[i] + (int64_t)kt * 128, base + (i * NW + wave) * 1024);
+    for (int i = 0; i < XLOADS; ++i) load_lds16(xsrc[i] + (int64_t)ktg * 128, base + (i * NW + wave) * 1024);
 #pragma unroll
     for (int i = 0; i < WLOADS; ++i) load_lds16(wsrc[i] + wk, base + XBYTES + (i * NW + wave) * 1024);
   };
@@ -874,7 +889,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_prefill_kernel(
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
 
   const int frow = lane & 31, h = lane >> 5;
-  const int KT = K / 64;
 #pragma unroll
   for (int p = 0; p < STAGES - 1; ++p)
     if (p < KT) issue_stage(p);
@@ -913,6 +927,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_prefill_kernel(
       }
     }
   }
+
+  if constexpr (SPLITK)
+    if (!split_k_reduce<TN, TM, NW>(acc, partials, counters, tile, split, splits, wave, lane, &is_last)) return;
 
   // Epilogue through LDS (as the FP8 kernel): lane l holds token l % 32 and, in
   // register r, channel 8*(r/4) + 4*(l/32) + r%4.
@@ -984,32 +1001,45 @@ __global__ __launch_bounds__(64 * WGM * WGN) void w8a16_prefill_kernel(
 template <int BM, int BN, int WGM, int WGN, int STAGES>
 static hipError_t launch_w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
                                        const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy, int group_m,
-                                       hipStream_t stream) {
+                                       hipStream_t stream, int splits = 1, float* partials = nullptr,
+                                       int* counters = nullptr) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-  const dim3 grid((unsigned)(tm * tn)), block(64 * WGM * WGN);
-  if (ldw == 0)
-    w8a16_prefill_kernel<BM, BN, WGM, WGN, STAGES, true><<<grid, block, 0, stream>>>(x, ldx, w, ldw, M, N, K, tm, tn,
-                                                                                     group_m, sw, bias, y, ldy);
-  else
-    w8a16_prefill_kernel<BM, BN, WGM, WGN, STAGES, false><<<grid, block, 0, stream>>>(x, ldx, w, ldw, M, N, K, tm, tn,
-                                                                                      group_m, sw, bias, y, ldy);
+  const dim3 grid((unsigned)(tm * tn * splits)), block(64 * WGM * WGN);
+#define JV_W8A16_PREFILL_LAUNCH(PW, SK)                                                                            \
+  w8a16_prefill_kernel<BM, BN, WGM, WGN, STAGES, PW, SK><<<grid, block, 0, stream>>>(x, ldx, w, ldw, M, N, K, tm, tn, \
+                                                                                      group_m, sw, bias, y, ldy,     \
+                                                                                      splits, partials, counters)
+  if (splits > 1) {
+    // K splits on the 64x64 tiles only
+    if constexpr (BM == 64 && BN == 64) {
+      if (ldw == 0) JV_W8A16_PREFILL_LAUNCH(true, true);
+      else JV_W8A16_PREFILL_LAUNCH(false, true);
+    } else {
+      return hipErrorInvalidValue;
+    }
+  } else if (ldw == 0) {
+    JV_W8A16_PREFILL_LAUNCH(true, false);
+  } else {
+    JV_W8A16_PREFILL_LAUNCH(false, false);
+  }
+#undef JV_W8A16_PREFILL_LAUNCH
   return hipGetLastError();
 }
 
 hipError_t w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
-                         const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy, int cu_count,
-                         hipStream_t stream) {
+                         const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy, int splits, float* partials,
+                         int* counters, int cu_count, hipStream_t stream) {
   if (K % 64) return hipErrorInvalidValue;
-  // 32-64 tokens over a wide weight (w8a16_decode_kernel_for): 64x64 tiles,
-  // four stages deep (gate+up at 32 tokens 31.3 us; three stages 34.5, six
-  // 34.7: each stage holds only 4 KB of weight).
-  if (M <= kDecodeMaxRows) return launch_w8a16_prefill<64, 64, 2, 2, 4>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 8, stream);
-  // Also where 128x128 tiles would not fill one round of CUs (q/o at 96
-  // tokens: 32 of them), except on the wide weights above: the 64x64 tiles
-  // give four times the workgroups.
-  const int64_t t128sq = ((int64_t)(M + 127) / 128) * ((N + 127) / 128);
-  if (t128sq < (int64_t)cu_count && 2 * ((N + 63) / 64) < 3 * (int64_t)cu_count)
-    return launch_w8a16_prefill<64, 64, 2, 2, 4>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 8, stream);
+  if (splits != w8a16_prefill_splits(M, N, K, cu_count) || (splits > 1 && (!partials || !counters)))
+    return hipErrorInvalidValue;
+  // 32-64 tokens over a wide weight (w8a16_decode_kernel_for), and wherever
+  // 128x128 tiles would not fill one round of CUs (q/o at 96 tokens: 32 of
+  // them) except on those wide weights: 64x64 tiles, four stages deep
+  // (gate+up at 32 tokens 31.3 us; three stages 34.5, six 34.7: each stage
+  // holds only 4 KB of weight), K split as w8a16_prefill_splits says.
+  if (w8a16_small_tiles(M, N, cu_count))
+    return launch_w8a16_prefill<64, 64, 2, 2, 4>(x, ldx, w, ldw, M, N, K, sw, bias, y, ldy, 8, stream, splits, partials,
+                                                 counters);
   // From five eighths of a round of 256x256 tiles on, 256x256 or 256x128
   // tiles, whichever needs less time in whole rounds: a round of 256x256
   // tiles takes 1.65 times one of 256x128 (123 / 73 us full at K = 4096, 101 /

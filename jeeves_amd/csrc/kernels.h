@@ -303,8 +303,45 @@ hipError_t w8a16_decode(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_
 hipError_t w8a16_batch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
                        const BatchPlan& p, const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy,
                        hipStream_t stream);
+// W8A16 prefill GEMM; `splits` must be w8a16_prefill_splits(M, N, K,
+// cu_count), with w8a16_prefill_partial_bytes of partials and
+// w8a16_prefill_counters zeroed tile counters when above 1.
 hipError_t w8a16_prefill(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, int M, int N, int K,
-                         const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy, int cu_count,
-                         hipStream_t stream);
+                         const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy, int splits, float* partials,
+                         int* counters, int cu_count, hipStream_t stream);
+
+// The W8A16 prefill kernel's 64x64 tiles: 32-64 tokens (wide weights, as
+// w8a16_decode_kernel_for sends them there), and wherever 128x128 tiles would
+// not fill one round of CUs except on weights of 1.5 rounds of 64-channel
+// tiles.
+inline bool w8a16_small_tiles(int64_t M, int64_t N, int cu_count) {
+  if (M <= kDecodeMaxRows) return true;
+  const int64_t t128sq = ((M + 127) / 128) * ((N + 127) / 128);
+  return t128sq < cu_count && 2 * ((N + 63) / 64) < 3 * (int64_t)cu_count;
+}
+
+// K splits of the 64x64 W8A16 prefill tiles where they fill at most a third
+// of the CUs: 3 or 4 splits, each keeping at least eight 64-deep stages (us,
+// graphs over rotated weights: k/v at 130 / 192 / 256 / 300 tokens 24.9 /
+// 25.0 / 24.9 / 25.0 -> 17.9 / 18.0 / 18.3 / 22.3; two splits of 128 tiles
+// measured slower, down at 96 tokens 67.7 -> 83.3, k/v at 512 25.2 -> 30.4).
+inline int w8a16_prefill_splits(int64_t M, int64_t N, int64_t K, int cu_count) {
+  if (!w8a16_small_tiles(M, N, cu_count) || K % 64) return 1;
+  const int64_t tiles = ((M + 63) / 64) * ((N + 63) / 64);
+  int64_t s = cu_count / tiles;
+  if (s < 3) return 1;
+  s = s > 4 ? 4 : s;
+  while (s > 1 && K / 64 < 8 * s) --s;
+  return (int)s;
+}
+
+// fp32 partial tiles and tile counters of a split W8A16 prefill launch.
+inline int64_t w8a16_prefill_partial_bytes(int64_t M, int64_t N, int64_t K, int cu_count) {
+  const int s = w8a16_prefill_splits(M, N, K, cu_count);
+  return s > 1 ? ((M + 63) / 64) * ((N + 63) / 64) * s * 64 * 64 * 4 : 0;
+}
+inline int64_t w8a16_prefill_counters(int64_t M, int64_t N, int64_t K, int cu_count) {
+  return w8a16_prefill_splits(M, N, K, cu_count) > 1 ? ((M + 63) / 64) * ((N + 63) / 64) : 0;
+}
 
 }  // namespace jv

@@ -59,10 +59,7 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _tile_counters(device: torch.device, M: int, N: int, K: int) -> torch.Tensor | None:
-    need = _lib.lib().jv_fp8_counters_needed(M, N, K, sm_count(device))
-    if need <= 0:
-        return None
+def _stream_counters(device: torch.device) -> torch.Tensor:
     # Launches on different streams can overlap and must not share tile
     # counters (inference/fp8.py:126), so they are kept per (device, stream).
     key = (device, _stream(device))
@@ -72,6 +69,14 @@ def _tile_counters(device: torch.device, M: int, N: int, K: int) -> torch.Tensor
             raise RuntimeError("run an fp8 GEMM on this stream before capturing a CUDA graph on it, so that the stream's tile "
                                "counters exist outside the graph")
         counters = TILE_COUNTERS[key] = torch.zeros(TILE_COUNTER_SLOTS, dtype=torch.int32, device=device)
+    return counters
+
+
+def _tile_counters(device: torch.device, M: int, N: int, K: int) -> torch.Tensor | None:
+    need = _lib.lib().jv_fp8_counters_needed(M, N, K, sm_count(device))
+    if need <= 0:
+        return None
+    counters = _stream_counters(device)
     if need > counters.numel():
         raise ValueError(f"{need} tiles exceed the {counters.numel()} tile counters")
     return counters
@@ -256,10 +261,12 @@ def fp8_matmul_w8a16(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
     scale = scale.to(torch.float32).contiguous()
     L = _lib.lib()
     with torch.cuda.device(dev):
-        counters = _tile_counters(dev, M, N, K)
         ws_bytes = L.jv_w8a16_workspace_bytes(M, N, K)
         if ws_bytes < 0:
             _lib.check(_lib.JV_ERR_HIP)
+        # a workspace means a K split (decode or prefill kernel), which counts
+        # its tiles in; the library checks that they fit the counters
+        counters = _stream_counters(dev) if ws_bytes > 0 else None
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         _lib.check(L.jv_w8a16_linear(x.data_ptr(), x.stride(0), w.data_ptr(), ldw, scale.data_ptr(),
                                      bias.data_ptr() if bias is not None else None, y.data_ptr(), N, M, N, K,

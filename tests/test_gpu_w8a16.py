@@ -198,6 +198,33 @@ def test_w8a16_batch_decode(N, K, M):
     assert oracle.within_metal_bound(oracle.bf16_to_f32(out), exact, magnitude * (BOUND_MAGNITUDE / 2.0 ** -20)), (N, M)
 
 
+# K split across workgroups on the prefill kernel's 64x64 tiles (at most a
+# third of a round of them): k/v at 129-320 tokens, a ragged 1040 channels,
+# a short k range (8 stages per split).
+@pytest.mark.parametrize("N,K,M", [(1024, 4096, 130), (1024, 4096, 256), (1024, 4096, 300), (1040, 4096, 200),
+                                   (1040, 4096, 300), (1024, 2048, 192)])
+def test_w8a16_split_prefill(N, K, M):
+    """The split form: the reference's Metal acceptance (>= 99.9% equal to the
+    fp32 math, the float64 bound), identical on a second call, tiled weights
+    equal to row-major ones, the bias bitwise."""
+    print(f"w8a16 split prefill N={N} K={K} M={M}", flush=True)
+    assert _lib.lib().jv_w8a16_workspace_bytes(M, N, K) > 0
+    g = torch.Generator().manual_seed(N + M + 1)
+    wq, sw = quantize_rows((torch.randn(N, K, generator=g) * 0.02).cuda())
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    bias = (torch.randn(N, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    y = fp8_matmul_w8a16(x, wq, sw)
+    assert torch.equal(fp8_matmul_w8a16(x, wq, sw), y), (N, M)
+    if N % 16 == 0:
+        assert torch.equal(fp8_matmul_w8a16(x, tile_weight(wq), sw, tiled=True), y), (N, M)
+    assert torch.equal(fp8_matmul_w8a16(x, wq, sw, bias=bias), y + bias), (N, M)
+    out = helpers.bits(y)
+    math = oracle.w8a16_math(helpers.bits(x), helpers.codes_np(wq), sw.cpu().numpy())
+    exact, magnitude = f64_parts(x, wq, sw)
+    assert oracle.bitwise_equal_fraction(out, math) >= MATH_EQUAL_MIN, (N, M)
+    assert oracle.within_metal_bound(oracle.bf16_to_f32(out), exact, magnitude * (BOUND_MAGNITUDE / 2.0 ** -20)), (N, M)
+
+
 @pytest.mark.parametrize("M", [16, 64, 256])
 def test_w8a16_every_code(M):
     """Every e4m3 code through the in-kernel widening: weight row n holds code
