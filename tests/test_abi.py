@@ -168,6 +168,35 @@ def test_batch_decode_plans_stay_within_their_bounds(product_lib):
     assert seen > 100, seen
 
 
+def test_prefill_plans_stay_within_their_bounds(product_lib):
+    """Over CU counts, weights and batch sizes above the decode regimes: a
+    ping-pong plan (kind 2) is one workgroup of 512 threads per 256x256 or
+    128x384 tile and never splits K; a lockstep plan (kind 1) runs 4 or 8
+    waves, and a K split keeps its tiles x splits within one round of
+    workgroups (at most two per CU) and needs one counter per tile."""
+    L = product_lib
+    seen_pp = seen_split = 0
+    for cus in (64, 80, 104, 120, 228, 256, 304):
+        for K in (2048, 4096, 12288):
+            for N in (1024, 1040, 4096, 6144, 10240, 12288, 24576):
+                for M in (129, 192, 300, 512, 777, 1024, 1536, 2048, 3000, 8192):
+                    kind, wgs, threads, splits = launch_shape(L, M, N, K, cus)
+                    assert kind in (1, 2), (cus, M, N, K, kind)
+                    if kind == 2:
+                        seen_pp += 1
+                        assert threads == 512 and splits == 1, (cus, M, N, K)
+                        assert wgs in (-(-M // 256) * -(-N // 256), -(-M // 128) * -(-N // 384)), (cus, M, N, K, wgs)
+                        continue
+                    assert threads in (256, 512) and 1 <= splits <= 8, (cus, M, N, K)
+                    if splits > 1:
+                        seen_split += 1
+                        assert wgs <= 2 * cus and wgs % splits == 0, (cus, M, N, K, wgs, splits)
+                        assert L.jv_fp8_counters_needed(M, N, K, cus) == wgs // splits
+                    else:
+                        assert L.jv_fp8_counters_needed(M, N, K, cus) == 0
+    assert seen_pp > 100 and seen_split > 20, (seen_pp, seen_split)
+
+
 def test_lockstep_model_picks_the_measured_fastest_tiles(product_lib):
     """Above 128 tokens the lockstep tile of least modelled time: the 5-stage
     64x128 / 64x64 rings where one round of small tiles is bound by the bytes
