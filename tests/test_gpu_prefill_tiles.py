@@ -19,7 +19,7 @@ import torch
 
 import oracle
 from jeeves_amd import _lib, synthetic
-from jeeves_amd.fp8 import fp8_matmul, gate_up_swiglu, swiglu_quantize, tile_weight
+from jeeves_amd.fp8 import fp8_matmul, fp8_matmul_quantized, gate_up_swiglu, swiglu_quantize, tile_weight
 from jeeves_amd.fp8_weights import quantize_rows
 from tests import helpers
 from tests.test_gpu_batch import amax_of, check, launch_shape
@@ -55,6 +55,9 @@ def test_128x384_tiles_oracle_and_other_plans(N, K, M):
     rows = sample_rows(M)
     check(y[rows], x[rows], wq, sw)
     assert torch.equal(fp8_matmul(x, wq, sw), y), "row-major weights differ"
+    xq, sx = quantize_rows(x)  # row-major activation codes (the kernel's unpacked token rows)
+    assert torch.equal(fp8_matmul_quantized(xq, sx, wt, sw, tiled=True), y), "row-major codes differ"
+    assert torch.equal(fp8_matmul_quantized(xq, sx, wq, sw), y), "row-major codes and weights differ"
     for short in (256, 384, 512, 192):  # a shorter batch on another plan without a K split
         kind, _, _, splits = launch_shape(short, N, K)
         if kind in (1, 2) and splits == 1 and not takes_128x384(short, N, K):
