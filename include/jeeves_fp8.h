@@ -206,7 +206,7 @@ int jv_fp8_linear_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw,
  * semantics, as jv_fp8_quantize_rows_bf16), for jv_fp8_gemm: codes in the
  * packed fragment order when ldc = 0, scales [M]; with lora_a [rank, I] bf16
  * also lora_t [M, rank] = h A^T in fp32. h_amax: the maxima
- * jv_fp8_linear_swiglu wrote for this h, or NULL. Decode batches (M <= 64)
+ * jv_fp8_linear_swiglu wrote for this h, or NULL. Decode batches (M <= 128)
  * in the packed layout without LoRA take each row's maximum from h_amax when
  * it is 8-byte aligned, so a row splits over several workgroups; h_amax must
  * then be exactly what jv_fp8_linear_swiglu stored with this h. Otherwise it

@@ -500,9 +500,10 @@ int jv_fp8_quantize_swiglu_output(const void* h, int64_t ldh, const uint16_t* h_
   if (packed && I % JV_FP8_BLOCK_K) return fail(JV_ERR_VALUE, "the packed layout needs I divisible by %d", JV_FP8_BLOCK_K);
   if (!aligned16(h) || (ldh * 2) % 16 || !aligned16(codes) || ldc % 16)
     return fail(JV_ERR_VALUE, "quantizing h needs 16-byte aligned rows");
-  // Decode batches split each row over workgroups when its maximum comes from
-  // h_amax; elsewhere the maximum is taken from h in the pass that encodes it.
-  if (h_amax && packed && lora_rank == 0 && M <= jv::kDecodeMaxRows && (reinterpret_cast<uintptr_t>(h_amax) & 7) == 0)
+  // Decode batches (up to 128 tokens) split each row over workgroups when its
+  // maximum comes from h_amax; elsewhere the maximum is taken from h in the
+  // pass that encodes it.
+  if (h_amax && packed && lora_rank == 0 && M <= 2 * jv::kDecodeMaxRows && (reinterpret_cast<uintptr_t>(h_amax) & 7) == 0)
     return hip_status(jv::quant_h_from_maxima((const uint16_t*)h, ldh, h_amax, M, (int)I, (uint8_t*)codes, scales,
                                               (hipStream_t)stream),
                       "quantization of h launch");

@@ -264,7 +264,7 @@ hipError_t quant_rows_bf16(const uint16_t* x, int64_t ldx, int64_t M, int K, uin
 hipError_t quant_swiglu_bf16(const uint16_t* gate, int64_t ldg, const uint16_t* up, int64_t ldu, int64_t M, int K,
                              uint8_t* codes, int64_t ldc, float* scales, uint16_t* h_out, int64_t ldh,
                              const uint16_t* lora_a, int rank, float* lora_t, bool packed, hipStream_t stream);
-// Packed codes of h for M <= kDecodeMaxRows rows from the SwiGLU epilogue's
+// Packed codes of h for M <= 2 kDecodeMaxRows rows from the SwiGLU epilogue's
 // maxima (parts [M, K/16], 8-byte aligned); K % 128 == 0, K <= 16384.
 hipError_t quant_h_from_maxima(const uint16_t* h, int64_t ldh, const uint16_t* parts, int64_t M, int K, uint8_t* codes,
                                float* scales, hipStream_t stream);

@@ -265,7 +265,7 @@ hipError_t quant_rows_bf16(const uint16_t* x, int64_t ldx, int64_t M, int K, uin
 hipError_t quant_h_from_maxima(const uint16_t* h, int64_t ldh, const uint16_t* parts, int64_t M, int K, uint8_t* codes,
                                float* scales, hipStream_t stream) {
   if (M == 0) return hipSuccess;
-  if (M > kDecodeMaxRows || K <= 0 || K > 16384 || (K & 127)) return hipErrorInvalidValue;
+  if (M > 2 * kDecodeMaxRows || K <= 0 || K > 16384 || (K & 127)) return hipErrorInvalidValue;
   const dim3 grid((unsigned)(K / 512 + (K % 512 != 0)), (unsigned)((M + 15) / 16 * 16));
   quant_h_maxima_kernel<<<grid, dim3(64), 0, stream>>>(h, ldh, parts, K, (int)M, codes, scales);
   return hipGetLastError();

@@ -106,9 +106,10 @@ def test_quantize_swiglu_output_equals_quantize_rows(M, rank):
 
 
 @pytest.mark.parametrize("I", [128, 1024, 4096, 12288, 16384])
-@pytest.mark.parametrize("M", [1, 5, 16, 17, 40, 64])
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 40, 64, 96, 128])
 def test_quantize_h_from_maxima_equals_one_pass(I, M):
-    """Decode batches quantize h from the epilogue's per-16-channel maxima,
+    """Decode batches (up to 128 tokens) quantize h from the epilogue's
+    per-16-channel maxima,
     each row split over workgroups: codes (padding rows included) and scales
     are the bits of the one-pass quantizer, which takes each row's maximum
     from h. Rows whose maximum sits in the first or last 16 channels, an inf,
@@ -132,17 +133,17 @@ def test_quantize_h_from_maxima_equals_one_pass(I, M):
     assert helpers.same_f32(got[1].cpu().numpy(), scales.cpu().numpy()).all(), (I, M)
 
 
-@pytest.mark.parametrize("M", [1, 64, 65, 300])
+@pytest.mark.parametrize("M", [1, 64, 65, 128, 129, 300])
 def test_maxima_are_read_only_for_decode_batches(M):
     """The dispatch: maxima that understate every row (all zero) change the
-    scales exactly where the quantizer reads them (M <= 64, packed, no LoRA)
+    scales exactly where the quantizer reads them (M <= 128, packed, no LoRA)
     and nowhere else, so the decode path really takes its maximum from them."""
     I = 4096
     h = synthetic.activations_heavy_tail(M, I, 8700 + M).cuda()
     zeros = torch.zeros(M, I // 16, dtype=torch.int16, device="cuda")
     want = quantize_swiglu_output(h, packed=True)
     got = quantize_swiglu_output(h, zeros, packed=True)
-    read = M <= 64
+    read = M <= 128
     assert torch.equal(got[1], want[1]) != read, M
     # LoRA and row-major codes never read the maxima
     a = synthetic.lora_factors(4096, I, 8701)[0].cuda()
@@ -150,7 +151,7 @@ def test_maxima_are_read_only_for_decode_batches(M):
     assert torch.equal(quantize_swiglu_output(h, zeros, packed=False)[1], want[1])
 
 
-@pytest.mark.parametrize("M", [1, 16, 64])
+@pytest.mark.parametrize("M", [1, 16, 64, 96, 128])
 def test_quantize_h_from_epilogue_maxima(M):
     """The maxima gate_up_swiglu stores, fed to the quantizer of h, give the
     bits of the quantizer that reads h alone; also through a misaligned view
